@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Benchmark of the Q4_K/Q6_K dequantize-matmul path on one MI355X.
+
+Workload (one "step" = one decoded token's projection sweep): a random-init
+Qwen3-4B Q4_K_M layout, 36 layers x {attn_q, attn_k (Q4_K 2560->4096/1024),
+attn_v (Q6_K 2560->1024), attn_output (Q4_K 4096->2560), ffn_gate, ffn_up
+(Q4_K 2560->9728), ffn_down (Q6_K 9728->2560)} + lm_head (Q6_K 2560->151936),
+M = 1 activation row, in the reference engine's call order
+(src/Engine.cpp:83-109): Q8 quantize + mat-vec per projection, SiLU*up before
+ffn_down. Weights (2.62 GB) are generated on the device; activations are
+N(0,1). The step is captured once as a graph and replayed.
+
+Prints one JSON line: value = algorithmic GB/s of the whole sweep
+(weights + fp32 activations in/out, see gemv_bytes), plus tokens/s, the
+roofline of the dominant kernel (per-launch HIP events) and the CPU oracle
+timed on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import pathlib
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PKG_DIR = ROOT / "qwen3-4b-q4_k_m-inference-engine_amd"
+
+Q4, Q6 = 12, 14
+SB_BYTES = {Q4: 144, Q6: 210}
+PEAK_HBM_GBS = 8000.0
+METRIC = "Q4_K/Q6_K GEMV HBM GB/s (% of peak) at M=1; decode tokens/s, 4B shapes"
+SEED = 20261205  # 20261201 + config id 4
+
+LAYER = [
+    ("attn_q", Q4, 2560, 4096),
+    ("attn_k", Q4, 2560, 1024),
+    ("attn_v", Q6, 2560, 1024),
+    ("attn_output", Q4, 4096, 2560),
+    ("ffn_gate", Q4, 2560, 9728),
+    ("ffn_up", Q4, 2560, 9728),
+    ("ffn_down", Q6, 9728, 2560),
+]
+LM_HEAD = ("lm_head", Q6, 2560, 151936)
+N_LAYERS = 36
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def load_package():
+    spec = importlib.util.spec_from_file_location("qk_amd", PKG_DIR / "__init__.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["qk_amd"] = mod
+    spec.loader.exec_module(mod)
+    mod.load()
+    return mod
+
+
+def gemv_bytes(qtype: int, K: int, N: int, M: int) -> int:
+    """Algorithmic HBM bytes of one mat-vec: packed weights + fp32 x + fp32 y."""
+    return N * (K // 256) * SB_BYTES[qtype] + 4 * M * K + 4 * M * N
+
+
+def kernel_family(qtype: int, K: int) -> str:
+    return f"{'Q4_K' if qtype == Q4 else 'Q6_K'} mat-vec K={K}"
+
+
+class DecodeSweep:
+    """Weights, activations and the per-token launch sequence of config 4."""
+
+    def __init__(self, qk, M: int = 1):
+        self.qk, self.M = qk, M
+        self.layers = []
+        tensor = 0
+        for _ in range(N_LAYERS):
+            layer = {}
+            for name, qtype, K, N in LAYER:
+                w = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
+                qk.synth_superblocks(w, qtype, N, K, SEED + 1000 * tensor, 0.01 if qtype == Q4 else 0.005, 0.01)
+                layer[name] = w
+                tensor += 1
+            self.layers.append(layer)
+        name, qtype, K, N = LM_HEAD
+        self.lm_head = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
+        qk.synth_superblocks(self.lm_head, qtype, N, K, SEED + 1000 * tensor, 0.005, 0.01)
+        buf = lambda n: qk.DeviceBuffer(4 * M * n)
+        self.x_attn, self.x_o, self.x_ffn = buf(2560), buf(4096), buf(2560)
+        qk.synth_normal(self.x_attn, M * 2560, SEED + 1)
+        qk.synth_normal(self.x_o, M * 4096, SEED + 2)
+        qk.synth_normal(self.x_ffn, M * 2560, SEED + 3)
+        self.y = {n: buf(N) for n, _, _, N in LAYER}
+        self.h = buf(9728)
+        self.logits = buf(LM_HEAD[3])
+        q8 = lambda k: qk.DeviceBuffer(M * (k // 32) * qk.Q8_BLOCK_BYTES)
+        self.q8_attn, self.q8_o, self.q8_ffn, self.q8_h = q8(2560), q8(4096), q8(2560), q8(9728)
+        qk.synchronize()
+
+    def launches(self):
+        """The mat-vec launches of one step: (name, qtype, K, N, weight, q8, y)."""
+        out = []
+        for layer in self.layers:
+            for name, qtype, K, N in LAYER:
+                q8 = {2560: self.q8_attn if name.startswith("attn") else self.q8_ffn,
+                      4096: self.q8_o, 9728: self.q8_h}[K]
+                out.append((name, qtype, K, N, layer[name], q8, self.y[name]))
+        name, qtype, K, N = LM_HEAD
+        out.append((name, qtype, K, N, self.lm_head, self.q8_attn, self.logits))
+        return out
+
+    def bytes_per_step(self) -> int:
+        return sum(gemv_bytes(q, K, N, self.M) for _, q, K, N, *_ in self.launches())
+
+    def record(self, stream, events=None) -> None:
+        """Enqueue one step; with `events`, bracket every mat-vec with an event pair."""
+        qk, M = self.qk, self.M
+        launches = iter(self.launches())
+
+        def gemv():
+            name, qtype, K, N, w, q8, y = next(launches)
+            if events is not None:
+                events[0].pop().record(stream)
+            qk.matmul_q8(q8, w, qtype, K, N, y, M, stream)
+            if events is not None:
+                events[1].pop().record(stream)
+
+        for _ in self.layers:
+            qk.quantize_q8(self.x_attn, M, 2560, self.q8_attn, stream)
+            gemv(), gemv(), gemv()                       # q, k, v
+            qk.quantize_q8(self.x_o, M, 4096, self.q8_o, stream)
+            gemv()                                       # attn_output
+            qk.quantize_q8(self.x_ffn, M, 2560, self.q8_ffn, stream)
+            gemv(), gemv()                               # gate, up
+            qk.silu_multiply(self.y["ffn_gate"], self.y["ffn_up"], self.h, M * 9728, stream)
+            qk.quantize_q8(self.h, M, 9728, self.q8_h, stream)
+            gemv()                                       # down
+        qk.quantize_q8(self.x_attn, M, 2560, self.q8_attn, stream)
+        gemv()                                           # lm_head
+
+
+def time_graph(qk, graph, stream, warmup: int, steps: int) -> float:
+    for _ in range(warmup):
+        graph.launch(stream)
+    stream.synchronize()
+    start, end = qk.Event(), qk.Event()
+    start.record(stream)
+    for _ in range(steps):
+        graph.launch(stream)
+    end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_ms(end)
+    start.destroy()
+    end.destroy()
+    return ms / steps
+
+
+def kernel_roofline(qk, sweep: DecodeSweep, stream, passes: int = 3):
+    """Per-launch HIP-event durations of every mat-vec of a step, per kernel family."""
+    launches = sweep.launches()
+    per_family: dict[str, dict] = {}
+    for _ in range(passes):
+        starts = [qk.Event() for _ in launches]
+        ends = [qk.Event() for _ in launches]
+        sweep.record(stream, events=(list(reversed(starts)), list(reversed(ends))))
+        stream.synchronize()
+        for (name, qtype, K, N, *_), a, b in zip(launches, starts, ends):
+            fam = per_family.setdefault(kernel_family(qtype, K), {"ms": 0.0, "bytes": 0, "launches": 0})
+            fam["ms"] += a.elapsed_ms(b)
+            fam["bytes"] += gemv_bytes(qtype, K, N, sweep.M)
+            fam["launches"] += 1
+        for e in starts + ends:
+            e.destroy()
+    out = {}
+    for fam, d in per_family.items():
+        avg_us = 1000.0 * d["ms"] / d["launches"]
+        avg_bytes = d["bytes"] / d["launches"]
+        gbs = avg_bytes / (avg_us * 1e3)
+        out[fam] = {"launches_per_step": d["launches"] // passes, "avg_us": round(avg_us, 3),
+                    "avg_bytes": int(avg_bytes), "GB/s": round(gbs, 1),
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "total_us_per_step": round(avg_us * d["launches"] / passes, 1)}
+    return out
+
+
+def cpu_baseline(qk, sweep: DecodeSweep, budget_s: float):
+    """The CPU oracle (OpenMP, double accumulation) on a bounded sample: the
+    projections of layer 0, repeated until ~budget_s of CPU work."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import qk_oracle  # checker only: CPU baseline leg
+
+    qk_oracle.load()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    rng_x = {K: qk_oracle.synth_normal(K, SEED + K) for K in (2560, 4096, 9728)}
+    weights = [(name, qtype, K, N, sweep.layers[0][name].download(np.uint8)) for name, qtype, K, N in LAYER]
+    done_bytes, elapsed, reps = 0, 0.0, 0
+    f32_bytes, f32_elapsed = 0, 0.0
+    while elapsed < budget_s or reps == 0:
+        for name, qtype, K, N, w in weights:
+            t0 = time.perf_counter()
+            qk_oracle.reference_product(rng_x[K], w, qtype, K, N, threads=threads)
+            elapsed += time.perf_counter() - t0
+            done_bytes += gemv_bytes(qtype, K, N, 1)
+        reps += 1
+    for name, qtype, K, N, w in weights:
+        t0 = time.perf_counter()
+        qk_oracle.reference_product_f32(rng_x[K], w, qtype, K, N, threads=threads)
+        f32_elapsed += time.perf_counter() - t0
+        f32_bytes += gemv_bytes(qtype, K, N, 1)
+    gbs = done_bytes / elapsed / 1e9
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"oracle reference_product (Q8 round trip, dequant, double accumulation) of the "
+                  f"7 layer-0 projections at M=1, repeated {reps}x ({elapsed:.1f} s)",
+        "tokens_per_s": round(gbs * 1e9 / sweep.bytes_per_step(), 3),
+        "fp32_accumulation_GB/s": round(f32_bytes / f32_elapsed / 1e9, 3),
+        "cpu": cpu,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--no-roofline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the path shards over output rows with no per-mat-vec exchange; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    qk = load_package()
+    info = qk.device_info()
+    log(f"device {info}")
+    t0 = time.perf_counter()
+    sweep = DecodeSweep(qk, M=1)
+    log(f"weights ready ({sweep.bytes_per_step() / 1e9:.3f} GB/step) in {time.perf_counter() - t0:.1f} s")
+    stream = qk.Stream()
+
+    # eager step (host-enqueued launch by launch), for reference
+    sweep.record(stream)
+    stream.synchronize()
+    e0 = time.perf_counter()
+    sweep.record(stream)
+    stream.synchronize()
+    eager_ms = (time.perf_counter() - e0) * 1e3
+
+    graph = qk.Graph.capture(stream, lambda: sweep.record(stream))
+    ms = time_graph(qk, graph, stream, args.warmup, args.steps)
+    bytes_step = sweep.bytes_per_step()
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    log(f"graph step {ms:.4f} ms -> {gbs:.1f} GB/s, {1e3 / ms:.1f} tok/s (eager step {eager_ms:.2f} ms)")
+
+    roofline, kernels = None, None
+    if not args.no_roofline:
+        kernels = kernel_roofline(qk, sweep, stream)
+        dominant = max(kernels, key=lambda k: kernels[k]["total_us_per_step"])
+        d = kernels[dominant]
+        roofline = {"bound": "hbm", "achieved": d["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": d["frac"], "traffic": None, "kernel": dominant,
+                    "avg_launch_us": d["avg_us"], "avg_bytes_per_launch": d["avg_bytes"]}
+        log(f"kernels: {json.dumps(kernels)}")
+
+    baseline = None
+    if args.cpu_seconds > 0:
+        log("CPU baseline (oracle, OpenMP) ...")
+        baseline = cpu_baseline(qk, sweep, args.cpu_seconds)
+        log(f"CPU baseline {baseline}")
+
+    graph.destroy()
+    stream.destroy()
+    line = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "Qwen3-4B Q4_K_M decode projection sweep, M=1: 36 x (q,k,v,o,gate,up,down) "
+                               "+ lm_head 151936x2560 Q6_K, Q8 activations, graph-replayed",
+                   "tokens_per_s": round(1e3 / ms, 2), "bytes_per_step": bytes_step,
+                   "frac_of_peak_hbm": round(gbs / PEAK_HBM_GBS, 4), "eager_ms_per_step": round(eager_ms, 3),
+                   "device": info["name"], "arch": info["arch"]},
+        "roofline": roofline,
+        "cpu_baseline": baseline,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

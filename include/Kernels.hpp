@@ -1,0 +1,71 @@
+#pragma once
+// Host-callable entry points for the Q4_K/Q6_K dequantize-matmul path, with the
+// signatures and semantics of the reference's include/Kernels.hpp:9-79
+// (kernels::matmul and its neighbours on this path). Float activations are
+// row-major device buffers; launches use the null stream unless a stream is
+// given. Errors surface as the reference's exception types. No HIP header is
+// included; calls go through the C-ABI of libqk_hip.so (include/qk_abi.h).
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "Weight.hpp"
+
+namespace kernels::detail {
+
+inline constexpr unsigned threads = 256;
+
+// Compute units of the current device (include/Kernels.hpp:15-26).
+int get_sm_count();
+
+// Turns a C-ABI status into the reference's exceptions: invalid arguments and
+// unsupported types -> std::invalid_argument (src/cuda/matmul.cu:132-136),
+// launch/runtime/allocation failures -> std::runtime_error
+// (include/Kernels.hpp:28-32, src/Weight.cpp:12-13).
+void check_status(int status, const char* what);
+
+}  // namespace kernels::detail
+
+namespace kernels {
+
+using stream_t = device_stream_t;
+
+// Non-blocking stream (include/Kernels.hpp:38-52, src/cuda/CudaStream.cpp:13-46).
+class Stream {
+public:
+    Stream();
+    ~Stream();
+    Stream(const Stream&) = delete;
+    Stream& operator=(const Stream&) = delete;
+    Stream(Stream&& other) noexcept;
+    Stream& operator=(Stream&& other) noexcept;
+
+    // Throws std::logic_error on a moved-from stream.
+    stream_t get() const;
+    void synchronize() const;
+    bool ready() const;
+
+private:
+    stream_t stream_{nullptr};
+};
+
+// The reference's name for the same class.
+using CudaStream = Stream;
+
+// output[rows x N] = Q8(input)[rows x K] . weight^T, K = weight.dimension[0],
+// N = weight.dimension[1]; output is overwritten (src/cuda/matmul.cu:130-165).
+void matmul(const float* input, const Weight& weight, float* output, size_t rows,
+    stream_t stream = nullptr);
+
+void matmul(const float* input, const Weight& weight, float* output, size_t rows,
+    const Stream& stream);
+
+// out = gate/(1+exp(-gate)) * up (src/cuda/silu_multiply.cu:19-23).
+void silu_multiply(const float* gate, const float* up, float* output, size_t count);
+
+// Superblock rows -> fp32 (src/cuda/embedding.cu:65-84).
+void dequantize_embeddings(const void* packed, float* output, size_t rows,
+    size_t width, size_t row_bytes, ggml_type type);
+
+}  // namespace kernels

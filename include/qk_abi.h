@@ -1,0 +1,164 @@
+/*
+ * qk_abi.h — C-ABI of the MI355X (gfx950) Q4_K/Q6_K dequantize-matmul library
+ * (libqk_hip.so). Plain pointers and sizes only: no HIP, CUDA or torch types.
+ *
+ * Conventions (src/cuda/matmul.cu:130-162, include/Kernels.hpp:9-10):
+ *   - x is a device fp32 row-major [M x K] activation matrix.
+ *   - w is the raw GGUF tensor bytes on the device: N rows, each K/256
+ *     superblocks (Q4_K: 144 bytes, Q6_K: 210 bytes), no repacking.
+ *     K = ggml ne[0] (Weight::dimension[0]), N = ne[1] (Weight::dimension[1]).
+ *   - y is a device fp32 row-major [M x N] output; it is overwritten.
+ *   - every launch is asynchronous on `stream` (NULL = the null stream).
+ *   - status: QK_OK, or an error code with a message in qk_last_error()
+ *     (thread-local, valid until the next failing call on the same thread).
+ */
+#ifndef QK_ABI_H
+#define QK_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum qk_status {
+    QK_OK = 0,
+    QK_ERR_INVALID_ARGUMENT = 1, /* std::invalid_argument in the C++ layer */
+    QK_ERR_UNSUPPORTED_TYPE = 2, /* std::invalid_argument in the C++ layer */
+    QK_ERR_RUNTIME = 3,          /* std::runtime_error in the C++ layer */
+    QK_ERR_OUT_OF_MEMORY = 4     /* std::runtime_error in the C++ layer */
+};
+
+/* GGUF on-disk tensor type ids (the values of ggml_type). */
+enum qk_type { QK_TYPE_F32 = 0, QK_TYPE_F16 = 1, QK_TYPE_Q4_K = 12, QK_TYPE_Q6_K = 14 };
+
+typedef void *qk_stream_t; /* a hipStream_t; NULL is the null stream */
+typedef void *qk_event_t;  /* a hipEvent_t */
+typedef void *qk_graph_t;  /* an instantiated hipGraphExec_t */
+
+/* Q8 activation block: 32 consecutive activations of one row.
+ * codes[i] = amax==0 ? 0 : (int8)roundf((x_i/amax)*127), scale = amax/127
+ * (the quantisation of src/cuda/matmul.cu:8-22), plus the sums the
+ * superblock dots need: scaled_sum = scale*sum(codes),
+ * neg32_sum_lo/hi = -32*sum(codes[0..15]) / -32*sum(codes[16..31]). */
+typedef struct qk_q8_block {
+    int8_t codes[32];
+    float scale;
+    float scaled_sum;
+    int32_t neg32_sum_lo;
+    int32_t neg32_sum_hi;
+} qk_q8_block;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *qk_last_error(void);
+/* Library version: major*10000 + minor*100 + patch. */
+int qk_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Dequantize-matmul (the hot path).
+ * ------------------------------------------------------------------------- */
+
+/* y[M x N] = Q8(x)[M x K] . W^T, allocating its workspace stream-ordered for
+ * the duration of the call. Replaces kernels::matmul
+ * (include/Kernels.hpp:57-61, src/cuda/matmul.cu:130-165). Validation as the
+ * reference: type must be Q4_K or Q6_K (else QK_ERR_UNSUPPORTED_TYPE),
+ * K > 0, K % 256 == 0, N > 0 (else QK_ERR_INVALID_ARGUMENT); M == 0 returns
+ * QK_OK without launching. */
+int qk_matmul(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
+              int64_t M, qk_stream_t stream);
+
+/* Workspace bytes qk_matmul_ws needs for this shape (0 when M == 0). */
+size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M);
+
+/* qk_matmul with a caller-owned device workspace of at least
+ * qk_matmul_workspace_size() bytes, 256-byte aligned. Allocates nothing, so it
+ * can be captured into a graph. Same semantics as qk_matmul otherwise. */
+int qk_matmul_ws(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
+                 int64_t M, void *workspace, size_t workspace_bytes, qk_stream_t stream);
+
+/* Step 1 of qk_matmul: x[M x K] -> M*K/32 qk_q8_block (K % 32 == 0).
+ * Replaces the quantize kernel of src/cuda/matmul.cu:8-22 (+ the sums). */
+int qk_quantize_q8(const float *x, int64_t M, int64_t K, qk_q8_block *q8,
+                   qk_stream_t stream);
+
+/* Step 2 of qk_matmul: y = q8 . W^T with q8 from qk_quantize_q8.
+ * Replaces project<Q4_K/Q6_K> of src/cuda/matmul.cu:86-125. */
+int qk_matmul_q8(const qk_q8_block *q8, const void *w, int type, int64_t K, int64_t N,
+                 float *y, int64_t M, qk_stream_t stream);
+
+/* Dequantize `rows` rows of K weights (row stride row_bytes) to fp32
+ * out[rows x K], bit-identical to the formulas of src/cuda/embedding.cu:6-59.
+ * Replaces kernels::dequantize_embeddings (include/Kernels.hpp:74-75,
+ * src/cuda/embedding.cu:65-84); rows == 0 returns QK_OK. */
+int qk_dequantize_rows(const void *packed, float *out, int64_t rows, int64_t K,
+                       size_t row_bytes, int type, qk_stream_t stream);
+
+/* out = gate/(1+exp(-gate)) * up, elementwise. Replaces kernels::silu_multiply
+ * (include/Kernels.hpp:72, src/cuda/silu_multiply.cu:19-23). */
+int qk_silu_multiply(const float *gate, const float *up, float *out, int64_t count,
+                     qk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Device memory, streams and events. The thin layer the C++ DeviceBuffer
+ * (include/Weight.hpp:8-23, src/Weight.cpp:6-51) and stream class
+ * (include/Kernels.hpp:38-52, src/cuda/CudaStream.cpp:13-46) sit on.
+ * ------------------------------------------------------------------------- */
+int qk_malloc(void **ptr, size_t bytes);
+int qk_free(void *ptr);
+int qk_malloc_async(void **ptr, size_t bytes, qk_stream_t stream);
+int qk_free_async(void *ptr, qk_stream_t stream);
+/* Host<->device copies are ordered on `stream` and complete before return. */
+int qk_memcpy_h2d(void *dst, const void *src, size_t bytes, qk_stream_t stream);
+int qk_memcpy_d2h(void *dst, const void *src, size_t bytes, qk_stream_t stream);
+int qk_memcpy_d2d_async(void *dst, const void *src, size_t bytes, qk_stream_t stream);
+int qk_memset_async(void *ptr, int value, size_t bytes, qk_stream_t stream);
+int qk_stream_create(qk_stream_t *stream); /* non-blocking stream */
+int qk_stream_destroy(qk_stream_t stream);
+int qk_stream_synchronize(qk_stream_t stream);
+int qk_stream_query(qk_stream_t stream, int *ready); /* *ready = 1 when idle */
+int qk_device_synchronize(void);
+int qk_device_count(int *count);
+int qk_set_device(int device);
+/* Name, compute units and arch of the current device (name_len bytes incl. NUL). */
+int qk_device_info(char *name, size_t name_len, int *compute_units, char *arch,
+                   size_t arch_len);
+int qk_event_create(qk_event_t *event);
+int qk_event_destroy(qk_event_t event);
+int qk_event_record(qk_event_t event, qk_stream_t stream);
+int qk_event_synchronize(qk_event_t event);
+int qk_event_elapsed_ms(float *ms, qk_event_t start, qk_event_t end);
+
+/* ---------------------------------------------------------------------------
+ * Graph capture of a launch sequence on a non-null stream, replayed with one
+ * call (the reference lists CUDA Graphs as future work, README.md:42). Only
+ * qk_quantize_q8, qk_matmul_q8, qk_matmul_ws and qk_silu_multiply may be
+ * captured: they allocate nothing and record no memset.
+ * ------------------------------------------------------------------------- */
+int qk_stream_begin_capture(qk_stream_t stream);
+/* Ends the capture and instantiates it; *graph owns the executable graph. */
+int qk_stream_end_capture(qk_stream_t stream, qk_graph_t *graph);
+int qk_graph_launch(qk_graph_t graph, qk_stream_t stream);
+int qk_graph_destroy(qk_graph_t graph);
+
+/* ---------------------------------------------------------------------------
+ * Synthetic inputs generated on the device (no host upload). No reference
+ * counterpart: the reference tests read the real model file
+ * (src/tests/TestModel.hpp.in:3). word(seed, i) is the i-th SplitMix64 output,
+ * mix64(seed + (i+1)*0x9E3779B97F4A7C15), and u24(w) = (w >> 40) * 2^-24.
+ *   Q4_K superblock b (row-major) uses words 20b..20b+19: d = fp16(u24(w0)*dmax),
+ *     dmin = fp16(u24(w1)*dminmax), scales = bytes 0..11 of w2,w3, qs = w4..w19.
+ *   Q6_K superblock b uses words 27b..27b+26: ql = w0..w15, qh = w16..w23,
+ *     scales[i] = int8((byte_i of w24,w25 & 127) - 64), d = fp16(u24(w26)*dmax).
+ *   Normal value i uses words 2i, 2i+1: Box-Muller in double with
+ *     u1 = 1 - u24(w_2i), u2 = u24(w_2i+1), z = sqrt(-2 ln u1) cos(2 pi u2).
+ * Bytes are little-endian; fp16 rounding is to nearest even.
+ * ------------------------------------------------------------------------- */
+int qk_synth_superblocks(void *w, int type, int64_t N, int64_t K, uint64_t seed, float dmax,
+                         float dminmax, qk_stream_t stream);
+int qk_synth_normal(float *x, int64_t count, uint64_t seed, qk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QK_ABI_H */

@@ -1,0 +1,363 @@
+// extern "C" entry points of libqk_hip.so (declared in include/qk_abi.h).
+// Validation mirrors kernels::matmul (src/cuda/matmul.cu:132-137) and
+// kernels::dequantize_embeddings (src/cuda/embedding.cu:67-70); launch errors
+// map to the codes the C++ layer turns into the reference's exceptions
+// (include/Kernels.hpp:28-32).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "qk_abi.h"
+#include "qk_launch.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& message) {
+  g_last_error = message;
+  return code;
+}
+
+int hip_fail(hipError_t error, const char* what) {
+  const int code = error == hipErrorOutOfMemory ? QK_ERR_OUT_OF_MEMORY : QK_ERR_RUNTIME;
+  return fail(code, std::string(what) + ": " + hipGetErrorString(error));
+}
+
+bool supported_type(int type) { return type == QK_TYPE_Q4_K || type == QK_TYPE_Q6_K; }
+
+size_t superblock_bytes(int type) {
+  return type == QK_TYPE_Q4_K ? 144u : type == QK_TYPE_Q6_K ? 210u : 0u;
+}
+
+// src/cuda/matmul.cu:132-137 (type, K > 0, K % 256 == 0, N > 0), plus the
+// launch-grid bound on rows the reference shares (grid.y = rows).
+int validate_matmul(int type, int64_t K, int64_t N, int64_t M) {
+  if (!supported_type(type))
+    return fail(QK_ERR_UNSUPPORTED_TYPE, "matmul supports Q4_K and Q6_K weights only");
+  if (K <= 0 || K % 256 != 0 || N <= 0 || N > (int64_t{1} << 31) - 8)
+    return fail(QK_ERR_INVALID_ARGUMENT, "Invalid matmul weight dimensions");
+  if (M < 0 || M > 65535)
+    return fail(QK_ERR_INVALID_ARGUMENT, "matmul rows must be in [0, 65535]");
+  return QK_OK;
+}
+
+size_t q8_bytes(int64_t M, int64_t K) {
+  return static_cast<size_t>(M) * static_cast<size_t>(K / 32) * sizeof(qk_q8_block);
+}
+
+hipStream_t as_stream(qk_stream_t s) { return static_cast<hipStream_t>(s); }
+
+int run_matmul(const float* x, const void* w, int type, int64_t K, int64_t N, float* y,
+               int64_t M, void* workspace, hipStream_t stream) {
+  auto* q8 = static_cast<qk_q8_block*>(workspace);
+  hipError_t error = qk::launch_quantize_q8(x, M, K, q8, stream);
+  if (error != hipSuccess) return hip_fail(error, "quantize launch failed");
+  error = qk::launch_gemv(q8, w, type, K, N, y, M, stream);
+  if (error != hipSuccess) return hip_fail(error, "matmul launch failed");
+  return QK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qk_last_error(void) { return g_last_error.c_str(); }
+
+int qk_version(void) { return 100; }
+
+size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M) {
+  if (!supported_type(type) || K <= 0 || K % 256 != 0 || N <= 0 || M <= 0) return 0;
+  return q8_bytes(M, K);
+}
+
+int qk_matmul(const float* x, const void* w, int type, int64_t K, int64_t N, float* y, int64_t M,
+              qk_stream_t stream) {
+  const int status = validate_matmul(type, K, N, M);
+  if (status != QK_OK) return status;
+  if (M == 0) return QK_OK;
+  if (!x || !w || !y) return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
+  const hipStream_t s = as_stream(stream);
+  void* workspace = nullptr;
+  hipError_t error = hipMallocAsync(&workspace, q8_bytes(M, K), s);
+  if (error != hipSuccess) return hip_fail(error, "hipMallocAsync failed");
+  const int result = run_matmul(x, w, type, K, N, y, M, workspace, s);
+  error = hipFreeAsync(workspace, s);
+  if (result != QK_OK) return result;
+  if (error != hipSuccess) return hip_fail(error, "hipFreeAsync failed");
+  return QK_OK;
+}
+
+int qk_matmul_ws(const float* x, const void* w, int type, int64_t K, int64_t N, float* y,
+                 int64_t M, void* workspace, size_t workspace_bytes, qk_stream_t stream) {
+  const int status = validate_matmul(type, K, N, M);
+  if (status != QK_OK) return status;
+  if (M == 0) return QK_OK;
+  if (!x || !w || !y || !workspace)
+    return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
+  if (workspace_bytes < q8_bytes(M, K))
+    return fail(QK_ERR_INVALID_ARGUMENT, "matmul workspace is smaller than qk_matmul_workspace_size");
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return fail(QK_ERR_INVALID_ARGUMENT, "matmul workspace must be 256-byte aligned");
+  return run_matmul(x, w, type, K, N, y, M, workspace, as_stream(stream));
+}
+
+int qk_quantize_q8(const float* x, int64_t M, int64_t K, qk_q8_block* q8, qk_stream_t stream) {
+  if (M < 0 || K <= 0 || K % 32 != 0)
+    return fail(QK_ERR_INVALID_ARGUMENT, "quantize needs M >= 0 and K a positive multiple of 32");
+  if (M == 0) return QK_OK;
+  if (!x || !q8) return fail(QK_ERR_INVALID_ARGUMENT, "quantize pointers must be non-null");
+  if (reinterpret_cast<uintptr_t>(q8) % 16 != 0)
+    return fail(QK_ERR_INVALID_ARGUMENT, "Q8 blocks must be 16-byte aligned");
+  const hipError_t error = qk::launch_quantize_q8(x, M, K, q8, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "quantize launch failed");
+}
+
+int qk_matmul_q8(const qk_q8_block* q8, const void* w, int type, int64_t K, int64_t N, float* y,
+                 int64_t M, qk_stream_t stream) {
+  const int status = validate_matmul(type, K, N, M);
+  if (status != QK_OK) return status;
+  if (M == 0) return QK_OK;
+  if (!q8 || !w || !y) return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
+  if (reinterpret_cast<uintptr_t>(q8) % 16 != 0)
+    return fail(QK_ERR_INVALID_ARGUMENT, "Q8 blocks must be 16-byte aligned");
+  const hipError_t error = qk::launch_gemv(q8, w, type, K, N, y, M, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "matmul launch failed");
+}
+
+int qk_dequantize_rows(const void* packed, float* out, int64_t rows, int64_t K, size_t row_bytes,
+                       int type, qk_stream_t stream) {
+  if (rows == 0) return QK_OK;  // src/cuda/embedding.cu:67
+  if (!supported_type(type))
+    return fail(QK_ERR_UNSUPPORTED_TYPE, "Unsupported embedding storage type");
+  if (rows < 0 || K <= 0 || K % 256 != 0 ||
+      row_bytes < static_cast<size_t>(K / 256) * superblock_bytes(type))
+    return fail(QK_ERR_INVALID_ARGUMENT, "Invalid dequantize dimensions");
+  if (!packed || !out) return fail(QK_ERR_INVALID_ARGUMENT, "dequantize pointers must be non-null");
+  const hipError_t error =
+      qk::launch_dequantize_rows(packed, out, rows, K, row_bytes, type, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "dequantize launch failed");
+}
+
+int qk_silu_multiply(const float* gate, const float* up, float* out, int64_t count,
+                     qk_stream_t stream) {
+  if (count < 0) return fail(QK_ERR_INVALID_ARGUMENT, "count must be >= 0");
+  if (count == 0) return QK_OK;  // src/cuda/silu_multiply.cu:20
+  if (!gate || !up || !out) return fail(QK_ERR_INVALID_ARGUMENT, "pointers must be non-null");
+  const hipError_t error = qk::launch_silu_multiply(gate, up, out, count, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "silu_multiply launch failed");
+}
+
+// ------------------------------------------------------------ memory shims --
+
+int qk_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(QK_ERR_INVALID_ARGUMENT, "null output pointer");
+  *ptr = nullptr;
+  if (bytes == 0) return QK_OK;  // src/Weight.cpp:27: empty buffers hold nullptr
+  const hipError_t error = hipMalloc(ptr, bytes);
+  return error == hipSuccess ? QK_OK : hip_fail(error, "hipMalloc failed");
+}
+
+int qk_free(void* ptr) {
+  if (!ptr) return QK_OK;
+  const hipError_t error = hipFree(ptr);
+  return error == hipSuccess ? QK_OK : hip_fail(error, "hipFree failed");
+}
+
+int qk_malloc_async(void** ptr, size_t bytes, qk_stream_t stream) {
+  if (!ptr) return fail(QK_ERR_INVALID_ARGUMENT, "null output pointer");
+  *ptr = nullptr;
+  if (bytes == 0) return QK_OK;
+  const hipError_t error = hipMallocAsync(ptr, bytes, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "hipMallocAsync failed");
+}
+
+int qk_free_async(void* ptr, qk_stream_t stream) {
+  if (!ptr) return QK_OK;
+  const hipError_t error = hipFreeAsync(ptr, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "hipFreeAsync failed");
+}
+
+int qk_memcpy_h2d(void* dst, const void* src, size_t bytes, qk_stream_t stream) {
+  if (bytes == 0) return QK_OK;
+  hipError_t error = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream));
+  if (error == hipSuccess) error = hipStreamSynchronize(as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "host-to-device copy failed");
+}
+
+int qk_memcpy_d2h(void* dst, const void* src, size_t bytes, qk_stream_t stream) {
+  if (bytes == 0) return QK_OK;
+  hipError_t error = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream));
+  if (error == hipSuccess) error = hipStreamSynchronize(as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "device-to-host copy failed");
+}
+
+int qk_memcpy_d2d_async(void* dst, const void* src, size_t bytes, qk_stream_t stream) {
+  if (bytes == 0) return QK_OK;
+  const hipError_t error =
+      hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "device-to-device copy failed");
+}
+
+int qk_memset_async(void* ptr, int value, size_t bytes, qk_stream_t stream) {
+  if (bytes == 0) return QK_OK;
+  const hipError_t error = hipMemsetAsync(ptr, value, bytes, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "memset failed");
+}
+
+int qk_stream_create(qk_stream_t* stream) {
+  if (!stream) return fail(QK_ERR_INVALID_ARGUMENT, "null output pointer");
+  hipStream_t s = nullptr;
+  const hipError_t error = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (error != hipSuccess) return hip_fail(error, "stream creation failed");
+  *stream = s;
+  return QK_OK;
+}
+
+int qk_stream_destroy(qk_stream_t stream) {
+  if (!stream) return QK_OK;
+  const hipError_t error = hipStreamDestroy(as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "stream destruction failed");
+}
+
+int qk_stream_synchronize(qk_stream_t stream) {
+  const hipError_t error = hipStreamSynchronize(as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "stream synchronize failed");
+}
+
+int qk_stream_query(qk_stream_t stream, int* ready) {
+  if (!ready) return fail(QK_ERR_INVALID_ARGUMENT, "null output pointer");
+  const hipError_t error = hipStreamQuery(as_stream(stream));
+  if (error == hipErrorNotReady) {
+    *ready = 0;
+    return QK_OK;
+  }
+  if (error != hipSuccess) return hip_fail(error, "stream query failed");
+  *ready = 1;
+  return QK_OK;
+}
+
+int qk_device_synchronize(void) {
+  const hipError_t error = hipDeviceSynchronize();
+  return error == hipSuccess ? QK_OK : hip_fail(error, "device synchronize failed");
+}
+
+int qk_device_count(int* count) {
+  if (!count) return fail(QK_ERR_INVALID_ARGUMENT, "null output pointer");
+  *count = 0;
+  const hipError_t error = hipGetDeviceCount(count);
+  if (error == hipErrorNoDevice) {
+    *count = 0;
+    return QK_OK;
+  }
+  return error == hipSuccess ? QK_OK : hip_fail(error, "device count failed");
+}
+
+int qk_set_device(int device) {
+  const hipError_t error = hipSetDevice(device);
+  return error == hipSuccess ? QK_OK : hip_fail(error, "set device failed");
+}
+
+int qk_device_info(char* name, size_t name_len, int* compute_units, char* arch, size_t arch_len) {
+  int device = 0;
+  hipError_t error = hipGetDevice(&device);
+  if (error != hipSuccess) return hip_fail(error, "get device failed");
+  hipDeviceProp_t prop;
+  error = hipGetDeviceProperties(&prop, device);
+  if (error != hipSuccess) return hip_fail(error, "device properties failed");
+  if (name && name_len) std::snprintf(name, name_len, "%s", prop.name);
+  if (arch && arch_len) std::snprintf(arch, arch_len, "%s", prop.gcnArchName);
+  if (compute_units) *compute_units = prop.multiProcessorCount;
+  return QK_OK;
+}
+
+int qk_event_create(qk_event_t* event) {
+  if (!event) return fail(QK_ERR_INVALID_ARGUMENT, "null output pointer");
+  hipEvent_t e = nullptr;
+  const hipError_t error = hipEventCreate(&e);
+  if (error != hipSuccess) return hip_fail(error, "event creation failed");
+  *event = e;
+  return QK_OK;
+}
+
+int qk_event_destroy(qk_event_t event) {
+  if (!event) return QK_OK;
+  const hipError_t error = hipEventDestroy(static_cast<hipEvent_t>(event));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "event destruction failed");
+}
+
+int qk_event_record(qk_event_t event, qk_stream_t stream) {
+  const hipError_t error = hipEventRecord(static_cast<hipEvent_t>(event), as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "event record failed");
+}
+
+int qk_event_synchronize(qk_event_t event) {
+  const hipError_t error = hipEventSynchronize(static_cast<hipEvent_t>(event));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "event synchronize failed");
+}
+
+int qk_event_elapsed_ms(float* ms, qk_event_t start, qk_event_t end) {
+  if (!ms) return fail(QK_ERR_INVALID_ARGUMENT, "null output pointer");
+  const hipError_t error =
+      hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "event elapsed time failed");
+}
+
+// ------------------------------------------------------------------ graphs --
+
+int qk_stream_begin_capture(qk_stream_t stream) {
+  if (!stream) return fail(QK_ERR_INVALID_ARGUMENT, "capture needs a non-null stream");
+  const hipError_t error = hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal);
+  return error == hipSuccess ? QK_OK : hip_fail(error, "begin capture failed");
+}
+
+int qk_stream_end_capture(qk_stream_t stream, qk_graph_t* graph) {
+  if (!stream || !graph) return fail(QK_ERR_INVALID_ARGUMENT, "capture needs a stream and an output");
+  *graph = nullptr;
+  hipGraph_t captured = nullptr;
+  hipError_t error = hipStreamEndCapture(as_stream(stream), &captured);
+  if (error != hipSuccess) return hip_fail(error, "end capture failed");
+  hipGraphExec_t exec = nullptr;
+  error = hipGraphInstantiate(&exec, captured, nullptr, nullptr, 0);
+  hipGraphDestroy(captured);
+  if (error != hipSuccess) return hip_fail(error, "graph instantiation failed");
+  *graph = exec;
+  return QK_OK;
+}
+
+int qk_graph_launch(qk_graph_t graph, qk_stream_t stream) {
+  if (!graph) return fail(QK_ERR_INVALID_ARGUMENT, "null graph");
+  const hipError_t error = hipGraphLaunch(static_cast<hipGraphExec_t>(graph), as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "graph launch failed");
+}
+
+int qk_graph_destroy(qk_graph_t graph) {
+  if (!graph) return QK_OK;
+  const hipError_t error = hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "graph destruction failed");
+}
+
+// -------------------------------------------------------------- synthetic --
+
+int qk_synth_superblocks(void* w, int type, int64_t N, int64_t K, uint64_t seed, float dmax,
+                         float dminmax, qk_stream_t stream) {
+  if (!supported_type(type)) return fail(QK_ERR_UNSUPPORTED_TYPE, "synth supports Q4_K and Q6_K");
+  if (N < 0 || K <= 0 || K % 256 != 0) return fail(QK_ERR_INVALID_ARGUMENT, "Invalid synth shape");
+  if (N == 0) return QK_OK;
+  if (!w) return fail(QK_ERR_INVALID_ARGUMENT, "synth pointer must be non-null");
+  const hipError_t error =
+      qk::launch_synth_superblocks(w, type, N, K, seed, dmax, dminmax, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "synth launch failed");
+}
+
+int qk_synth_normal(float* x, int64_t count, uint64_t seed, qk_stream_t stream) {
+  if (count < 0) return fail(QK_ERR_INVALID_ARGUMENT, "count must be >= 0");
+  if (count == 0) return QK_OK;
+  if (!x) return fail(QK_ERR_INVALID_ARGUMENT, "synth pointer must be non-null");
+  const hipError_t error = qk::launch_synth_normal(x, count, seed, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "synth launch failed");
+}
+
+}  // extern "C"

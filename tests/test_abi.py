@@ -1,0 +1,98 @@
+"""CPU checks of the drop-in boundary: libqk_hip.so loads, exports every symbol
+include/qk_abi.h declares, and validates arguments on the host exactly like
+kernels::matmul (src/cuda/matmul.cu:132-137) before touching the device.
+No compute call is made: every call here returns before any HIP call."""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "qk_abi.h"
+
+
+def declared_functions(header: pathlib.Path) -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(qk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(qk):
+    names = declared_functions(HEADER)
+    assert len(names) >= 30
+    lib = ctypes.CDLL(str(qk.library_path()))
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert sorted(qk.declared_symbols()) == names
+
+
+def test_engine_library_links_the_c_abi(qk):
+    path = qk.ENGINE_PATH
+    assert path.exists()
+    out = subprocess.run(["nm", "-D", "--undefined-only", str(path)], capture_output=True,
+                         text=True, check=True).stdout
+    used = set(re.findall(r"\b(qk_[a-z0-9_]+)\b", out))
+    assert {"qk_matmul", "qk_malloc_async", "qk_stream_create", "qk_last_error"} <= used
+    # the host layer reaches HIP only through the C-ABI
+    assert "hipLaunchKernel" not in out and "hipMalloc" not in out
+
+
+def test_version_and_last_error_start_clean(qk):
+    lib = qk.load()
+    assert lib.qk_version() >= 100
+    assert lib.qk_last_error() == b""
+
+
+@pytest.mark.parametrize("qtype,K,N,M,code", [
+    (13, 2560, 8, 1, 2),        # Q5_K: unsupported type
+    (0, 2560, 8, 1, 2),         # F32
+    (12, 2500, 8, 1, 1),        # K not a multiple of 256
+    (12, 0, 8, 1, 1),           # K = 0
+    (14, -256, 8, 1, 1),        # K < 0
+    (12, 2560, 0, 1, 1),        # N = 0
+    (14, 2560, -3, 1, 1),       # N < 0
+    (12, 2560, 8, -1, 1),       # negative rows
+    (12, 2560, 8, 70000, 1),    # rows beyond the launch grid
+])
+def test_matmul_validation_matches_reference(qk, qtype, K, N, M, code):
+    lib = qk.load()
+    status = lib.qk_matmul(None, None, qtype, K, N, None, M, None)
+    assert status == code
+    msg = lib.qk_last_error().decode()
+    assert ("Q4_K and Q6_K" in msg) if code == 2 else ("dimensions" in msg or "rows" in msg)
+    assert lib.qk_matmul_q8(None, None, qtype, K, N, None, M, None) == code
+    assert lib.qk_matmul_ws(None, None, qtype, K, N, None, M, None, 0, None) == code
+
+
+def test_zero_rows_is_a_no_op(qk):
+    lib = qk.load()
+    assert lib.qk_matmul(None, None, 12, 2560, 8, None, 0, None) == 0
+    assert lib.qk_matmul_q8(None, None, 14, 9728, 8, None, 0, None) == 0
+    assert lib.qk_dequantize_rows(None, None, 0, 2560, 1440, 99, None) == 0
+    assert lib.qk_silu_multiply(None, None, None, 0, None) == 0
+
+
+def test_other_validation(qk):
+    lib = qk.load()
+    assert lib.qk_dequantize_rows(None, None, 1, 2560, 1440, 13, None) == 2
+    assert lib.qk_dequantize_rows(None, None, 1, 2560, 1000, 12, None) == 1  # stride < row
+    assert lib.qk_matmul(None, None, 12, 2560, 8, None, 1, None) == 1      # null pointers
+    assert lib.qk_quantize_q8(None, 1, 100, None, None) == 1
+    assert lib.qk_matmul_workspace_size(12, 2560, 8, 3) == 3 * 80 * 48
+    assert lib.qk_matmul_workspace_size(12, 2560, 8, 0) == 0
+    assert lib.qk_matmul_workspace_size(13, 2560, 8, 1) == 0
+    ws = ctypes.c_void_p(256)
+    assert lib.qk_matmul_ws(ctypes.c_void_p(16), ctypes.c_void_p(16), 12, 2560, 8,
+                            ctypes.c_void_p(16), 1, ws, 10, None) == 1  # workspace too small
+
+
+def test_cpp_host_layer_validation():
+    """tests/cpp/host_tests.cpp: kernels::matmul throws the reference's exception types."""
+    exe = ROOT / "qwen3-4b-q4_k_m-inference-engine_amd" / "_build" / "host_tests"
+    assert exe.exists(), "build the package first"
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    print(res.stdout[-2000:], res.stderr[-2000:])
+    assert res.returncode == 0

@@ -1,0 +1,311 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C-ABI.
+
+Bars: dequantized weights bit-exact; matmul outputs
+within max |y - y_ref| / ||y_ref[m,:]||_2 <= 1e-3 of the oracle's
+double-accumulated product. The reference's own per-element criterion,
+Catch2 Approx(eps=1e-4, margin=3e-5) (src/tests/reference/MatmulReference.hpp:71-78),
+is asserted as well. The contract cases mirror src/tests/MatmulTests.cpp:
+overwrite on reuse, sentinels around an offset output, zero input -> exact
+zeros, two concurrent streams, rows in {1, 4, 5, 101}, truncated N.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from ggml_layout import f16_bits, pack_q4k, pack_q6k
+
+pytestmark = pytest.mark.gpu
+
+Q4, Q6 = 12, 14
+ROW_NORM_BAR = 1e-3
+SEED = 20261201
+
+# Qwen3-4B projections: name -> (type, K, N)
+SHAPES = {
+    "attn_q": (Q4, 2560, 4096),
+    "attn_k": (Q4, 2560, 1024),
+    "attn_v": (Q6, 2560, 1024),
+    "attn_output": (Q4, 4096, 2560),
+    "ffn_gate": (Q4, 2560, 9728),
+    "ffn_up": (Q4, 2560, 9728),
+    "ffn_down": (Q6, 9728, 2560),
+    "lm_head": (Q6, 2560, 151936),
+}
+DMAX = {Q4: 0.01, Q6: 0.005}
+
+
+def make_weight(qk, oracle, qtype, N, K, seed):
+    """Superblocks generated on the device; the oracle regenerates the same bytes."""
+    w = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
+    qk.synth_superblocks(w, qtype, N, K, seed, DMAX[qtype], 0.01)
+    qk.synchronize()
+    return w
+
+
+def run_matmul(qk, w, qtype, K, N, x_host, M):
+    x = qk.DeviceBuffer.from_array(x_host.astype(np.float32))
+    y = qk.DeviceBuffer(M * N * 4)
+    qk.matmul(x, w, qtype, K, N, y, M)
+    qk.synchronize()
+    return y.download(np.float32, M * N).reshape(M, N)
+
+
+def assert_parity(oracle, got, ref, approx_floor=0.999):
+    err = oracle.row_norm_error(got, ref)
+    rate = oracle.approx_pass_rate(got, ref)
+    print(f"row-norm error {err:.3e}, Approx pass rate {rate:.5f}", flush=True)
+    assert err <= ROW_NORM_BAR
+    assert err <= 1e-5  # integer dots + fp32 epilogue: far inside the bar
+    assert rate >= approx_floor
+
+
+# ------------------------------------------------------------- synthetic --
+
+@pytest.mark.parametrize("qtype,N,K", [(Q4, 9728, 2560), (Q6, 2560, 9728)])
+def test_device_synth_matches_oracle_bytes(gpu, oracle, qtype, N, K):
+    w = make_weight(gpu, oracle, qtype, N, K, SEED)
+    got = w.download(np.uint8)
+    ref = oracle.synth_superblocks(qtype, N, K, SEED, DMAX[qtype], 0.01)
+    assert np.array_equal(got, ref)
+
+
+def test_device_synth_normal(gpu, oracle):
+    x = gpu.DeviceBuffer(4 * 100000)
+    gpu.synth_normal(x, 100000, 77)
+    gpu.synchronize()
+    got = x.download(np.float32)
+    ref = oracle.synth_normal(100000, 77)
+    assert np.allclose(got, ref, rtol=1e-6, atol=1e-6)
+
+
+# --------------------------------------------------------------- dequant --
+
+@pytest.mark.parametrize("qtype,N,K", [(Q4, 9728, 2560), (Q6, 2560, 9728)])
+def test_dequantize_bit_exact_full_matrix(gpu, oracle, qtype, N, K):
+    w = make_weight(gpu, oracle, qtype, N, K, SEED + 1)
+    out = gpu.DeviceBuffer(N * K * 4)
+    gpu.dequantize_rows(w, out, N, K, gpu.row_bytes(qtype, K), qtype)
+    gpu.synchronize()
+    got = out.download(np.float32)
+    ref = oracle.dequantize(w.download(np.uint8), qtype, N, K).ravel()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def _special_blocks():
+    rng = np.random.default_rng(5)
+    q4 = [
+        pack_q4k(0x0001, 0x0001, rng.integers(0, 64, 8), rng.integers(0, 64, 8), rng.integers(0, 16, 256)),
+        pack_q4k(0, 0, [63] * 8, [63] * 8, [15] * 256),
+        pack_q4k(0x7BFF, 0x7BFF, [63] * 8, [63] * 8, [15] * 256),     # largest finite d
+        pack_q4k(f16_bits(1.0), f16_bits(1.0), rng.integers(0, 64, 8), rng.integers(0, 64, 8),
+                 rng.integers(0, 16, 256)),
+        pack_q4k(0x03FF, 0x0200, rng.integers(0, 64, 8), rng.integers(0, 64, 8), rng.integers(0, 16, 256)),
+    ]
+    q6 = [
+        pack_q6k(rng.integers(0, 64, 256), rng.integers(-128, 128, 16), 0x0001),
+        pack_q6k([0] * 256, [-128] * 16, 0x7BFF),
+        pack_q6k([63] * 256, [127] * 16, 0x7BFF),
+        pack_q6k(rng.integers(0, 64, 256), rng.integers(-128, 128, 16), 0x8001),  # negative subnormal d
+        pack_q6k(rng.integers(0, 64, 256), rng.integers(-128, 128, 16), f16_bits(1.0)),
+    ]
+    return q4, q6
+
+
+@pytest.mark.parametrize("which", [0, 1])
+def test_dequantize_special_blocks(gpu, oracle, which):
+    qtype = (Q4, Q6)[which]
+    blocks = _special_blocks()[which]
+    packed = np.frombuffer(b"".join(blocks), dtype=np.uint8)
+    K = 256 * len(blocks)
+    w = gpu.DeviceBuffer.from_array(packed)
+    out = gpu.DeviceBuffer(K * 4)
+    gpu.dequantize_rows(w, out, 1, K, len(packed), qtype)
+    gpu.synchronize()
+    got = out.download(np.float32)
+    ref = oracle.dequantize(packed, qtype, 1, K).ravel()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequantize_strided_rows_into_offset_output(gpu, oracle):
+    """Gathered embedding rows: row stride > packed bytes, output at +1 float."""
+    qtype, K, rows, stride = Q6, 2560, 7, 2100 + 44
+    host = np.zeros((rows, stride), np.uint8)
+    host[:, :2100] = oracle.synth_superblocks(qtype, rows, K, 99, 0.005).reshape(rows, 2100)
+    w = gpu.DeviceBuffer.from_array(host.ravel())
+    out = gpu.DeviceBuffer((rows * K + 2) * 4)
+    out.upload(np.full(rows * K + 2, 123.0, np.float32))
+    gpu.dequantize_rows(w, out.ptr + 4, rows, K, stride, qtype)
+    gpu.synchronize()
+    got = out.download(np.float32)
+    assert got[0] == 123.0 and got[-1] == 123.0
+    ref = oracle.dequantize(host.ravel(), qtype, rows, K, stride=stride).ravel()
+    assert np.array_equal(got[1:-1].view(np.uint32), ref.view(np.uint32))
+
+
+# --------------------------------------------------------------------- Q8 --
+
+def test_quantize_q8_matches_oracle(gpu, oracle):
+    M, K = 5, 9728
+    x = oracle.synth_normal(M * K, 123)
+    x[:64] = 0.0
+    xd = gpu.DeviceBuffer.from_array(x)
+    q8 = gpu.DeviceBuffer(M * K // 32 * gpu.Q8_BLOCK_BYTES)
+    gpu.quantize_q8(xd, M, K, q8)
+    gpu.synchronize()
+    blocks = q8.download(np.uint8).view(gpu.Q8_DTYPE)
+    codes, scales = oracle.quantize_q8(x)
+    assert np.array_equal(blocks["codes"].ravel(), codes)
+    assert np.array_equal(blocks["scale"].view(np.uint32), scales.view(np.uint32))
+    c = codes.reshape(-1, 32).astype(np.int64)
+    assert np.array_equal(blocks["neg32_sum_lo"], -32 * c[:, :16].sum(1))
+    assert np.array_equal(blocks["neg32_sum_hi"], -32 * c[:, 16:].sum(1))
+    assert np.allclose(blocks["scaled_sum"], scales * c.sum(1), rtol=1e-6, atol=0)
+
+
+# ----------------------------------------------------------------- matmul --
+
+@pytest.mark.parametrize("name", list(SHAPES))
+def test_matmul_m1_qwen3_shapes(gpu, oracle, name):
+    qtype, K, N = SHAPES[name]
+    print(f"[case] {name} type={qtype} K={K} N={N} M=1", flush=True)
+    w = make_weight(gpu, oracle, qtype, N, K, SEED + 100 + list(SHAPES).index(name))
+    x = oracle.synth_normal(K, SEED + 7)
+    got = run_matmul(gpu, w, qtype, K, N, x, 1)
+    ref = oracle.reference_product(x, w.download(np.uint8), qtype, K, N)
+    assert_parity(oracle, got, ref)
+
+
+@pytest.mark.parametrize("qtype,K", [(Q4, 2560), (Q6, 2560), (Q4, 4096), (Q6, 9728)])
+@pytest.mark.parametrize("rows", [1, 4, 5, 101])
+def test_matmul_rows_truncated_columns(gpu, oracle, qtype, K, rows):
+    """src/tests/MatmulTests.cpp:165-213: N = 19 of a larger tensor, sentinels."""
+    print(f"[case] type={qtype} K={K} rows={rows}", flush=True)
+    N_full, N = 64, 19
+    w = make_weight(gpu, oracle, qtype, N_full, K, SEED + 3)
+    x = np.sin(np.arange(rows * K, dtype=np.float32) * np.float32(0.031)).astype(np.float32) * np.float32(0.1)
+    xd = gpu.DeviceBuffer.from_array(x)
+    out = gpu.DeviceBuffer((rows * N + 2) * 4)
+    out.upload(np.full(rows * N + 2, 123.0, np.float32))
+    stream = gpu.Stream()
+    ref = oracle.reference_product(x, w.download(np.uint8)[: N * gpu.row_bytes(qtype, K)], qtype, K, N)
+    for _ in range(2):
+        gpu.matmul(xd, w, qtype, K, N, out, rows, stream, y_offset=4)
+        stream.synchronize()
+        got = out.download(np.float32)
+        assert got[0] == 123.0 and got[-1] == 123.0
+        assert_parity(oracle, got[1:-1], ref, approx_floor=1.0)
+    xd.fill(0)
+    gpu.matmul(xd, w, qtype, K, N, out, rows, None, y_offset=4)
+    gpu.synchronize()
+    got = out.download(np.float32)
+    assert np.all(got[1:-1] == 0.0)
+    assert got[0] == 123.0 and got[-1] == 123.0
+    stream.destroy()
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6])
+def test_matmul_overwrite_and_concurrent_streams(gpu, oracle, qtype):
+    """src/tests/MatmulTests.cpp:93-163 on synthetic weights (K full width, N = 5, M = 3)."""
+    K, N, M = (2560, 5, 3)
+    w = make_weight(gpu, oracle, qtype, 16, K, SEED + 4)
+    x = np.sin(np.arange(M * K, dtype=np.float32) * np.float32(0.031)).astype(np.float32) * np.float32(0.1)
+    ref = oracle.reference_product(x, w.download(np.uint8)[: N * gpu.row_bytes(qtype, K)], qtype, K, N)
+    xd = gpu.DeviceBuffer.from_array(x)
+    y1 = gpu.DeviceBuffer.from_array(np.full(M * N, 123.0, np.float32))
+    y2 = gpu.DeviceBuffer.from_array(np.full(M * N, 123.0, np.float32))
+    for _ in range(2):
+        gpu.matmul(xd, w, qtype, K, N, y1, M)
+        gpu.synchronize()
+        got = y1.download(np.float32)
+        assert oracle.approx_pass_rate(got, ref, margin=1e-5) == 1.0
+    s1, s2 = gpu.Stream(), gpu.Stream()
+    gpu.matmul(xd, w, qtype, K, N, y1, M, s1)
+    gpu.matmul(xd, w, qtype, K, N, y2, M, s2)
+    s1.synchronize()
+    s2.synchronize()
+    a, b = y1.download(np.float32), y2.download(np.float32)
+    assert np.array_equal(a, b)
+    assert oracle.approx_pass_rate(a, ref, margin=1e-5) == 1.0
+    xd.fill(0)
+    gpu.matmul(xd, w, qtype, K, N, y1, 1)
+    gpu.synchronize()
+    assert np.all(y1.download(np.float32, N) == 0.0)
+    s1.destroy()
+    s2.destroy()
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6])
+@pytest.mark.parametrize("K", [256, 512, 768, 1280, 3328])
+def test_matmul_generic_widths(gpu, oracle, qtype, K):
+    N, M = 45, 3
+    w = make_weight(gpu, oracle, qtype, N, K, SEED + K)
+    x = oracle.synth_normal(M * K, SEED + 8)
+    got = run_matmul(gpu, w, qtype, K, N, x, M)
+    ref = oracle.reference_product(x, w.download(np.uint8), qtype, K, N)
+    assert_parity(oracle, got, ref)
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6])
+def test_matmul_entry_points_agree_bitwise(gpu, oracle, qtype):
+    """qk_matmul, qk_matmul_ws and qk_quantize_q8 + qk_matmul_q8 give identical bits."""
+    K, N, M = 2560, 1000, 2
+    w = make_weight(gpu, oracle, qtype, N, K, SEED + 9)
+    x = oracle.synth_normal(M * K, SEED + 10)
+    a = run_matmul(gpu, w, qtype, K, N, x, M)
+    xd = gpu.DeviceBuffer.from_array(x)
+    ws_bytes = gpu.matmul_workspace_size(qtype, K, N, M)
+    ws = gpu.DeviceBuffer(ws_bytes)
+    y = gpu.DeviceBuffer(M * N * 4)
+    gpu.matmul_ws(xd, w, qtype, K, N, y, M, ws, ws_bytes)
+    gpu.synchronize()
+    b = y.download(np.float32).reshape(M, N)
+    gpu.quantize_q8(xd, M, K, ws)
+    gpu.matmul_q8(ws, w, qtype, K, N, y, M)
+    gpu.synchronize()
+    c = y.download(np.float32).reshape(M, N)
+    assert np.array_equal(a, b) and np.array_equal(a, c)
+
+
+def test_silu_multiply(gpu, oracle):
+    n = 9728 * 3
+    g = oracle.synth_normal(n, 11) * 4
+    u = oracle.synth_normal(n, 12)
+    gd, ud = gpu.DeviceBuffer.from_array(g), gpu.DeviceBuffer.from_array(u)
+    od = gpu.DeviceBuffer(n * 4)
+    gpu.silu_multiply(gd, ud, od, n)
+    gpu.synchronize()
+    assert np.allclose(od.download(np.float32), oracle.silu_multiply(g, u), rtol=2e-6, atol=1e-7)
+
+
+def test_graph_replay_matches_eager(gpu, oracle):
+    """A captured quantize + mat-vec sequence, replayed several times with eager
+    work and synchronizations in between; every replay equals the eager result."""
+    qk = gpu
+    shapes = [(Q4, 2560, 4096), (Q6, 2560, 1024), (Q4, 4096, 2560), (Q6, 9728, 2560)]
+    ws = [make_weight(qk, oracle, q, N, K, SEED + 500 + i) for i, (q, K, N) in enumerate(shapes)]
+    xs = {K: qk.DeviceBuffer.from_array(oracle.synth_normal(K, SEED + K)) for K in (2560, 4096, 9728)}
+    q8 = {K: qk.DeviceBuffer(K // 32 * qk.Q8_BLOCK_BYTES) for K in xs}
+    ys = [qk.DeviceBuffer(4 * N) for _, _, N in shapes]
+    stream = qk.Stream()
+
+    def record():
+        for (q, K, N), w, y in zip(shapes, ws, ys):
+            qk.quantize_q8(xs[K], 1, K, q8[K], stream)
+            qk.matmul_q8(q8[K], w, q, K, N, y, 1, stream)
+
+    record()
+    stream.synchronize()
+    eager = [y.download(np.float32) for y in ys]
+    graph = qk.Graph.capture(stream, record)
+    for rep in range(4):
+        for y in ys:
+            y.upload(np.full(y.nbytes // 4, np.nan, np.float32))
+        graph.launch(stream)
+        stream.synchronize()
+        for e, y in zip(eager, ys):
+            assert np.array_equal(y.download(np.float32), e), f"replay {rep}"
+        record()  # eager work between replays
+        stream.synchronize()
+    graph.destroy()
+    stream.destroy()
