@@ -68,12 +68,19 @@ def gemv_bytes(qtype: int, K: int, N: int, M: int) -> int:
     return N * (K // 256) * SB_BYTES[qtype] + 4 * M * K + 4 * M * N
 
 
-def kernel_family(qtype: int, K: int) -> str:
-    return f"{'Q4_K' if qtype == Q4 else 'Q6_K'} mat-vec K={K}"
+def weight_bytes(qtype: int, K: int, N: int) -> int:
+    return N * (K // 256) * SB_BYTES[qtype]
+
+
+class Op:
+    """One launch of the step: a kernel family name, its algorithmic bytes and the call."""
+
+    def __init__(self, family: str, nbytes: int, call):
+        self.family, self.nbytes, self.call = family, nbytes, call
 
 
 class DecodeSweep:
-    """Weights, activations and the per-token launch sequence of config 4."""
+    """Weights, activations and the per-token launch sequence of the decode sweep."""
 
     def __init__(self, qk, M: int = 1):
         self.qk, self.M = qk, M
@@ -98,50 +105,39 @@ class DecodeSweep:
         self.y = {n: buf(N) for n, _, _, N in LAYER}
         self.h = buf(9728)
         self.logits = buf(LM_HEAD[3])
-        q8 = lambda k: qk.DeviceBuffer(M * (k // 32) * qk.Q8_BLOCK_BYTES)
-        self.q8_attn, self.q8_o, self.q8_ffn, self.q8_h = q8(2560), q8(4096), q8(2560), q8(9728)
         qk.synchronize()
 
-    def launches(self):
-        """The mat-vec launches of one step: (name, qtype, K, N, weight, q8, y)."""
+    def ops(self, stream):
+        """The launches of one step, in the reference engine's order
+        (src/Engine.cpp:83-109): q/k/v in one launch, attn_output, gate/up with
+        SiLU*up in one launch, ffn_down; then lm_head."""
+        qk, M, y = self.qk, self.M, self.y
         out = []
         for layer in self.layers:
-            for name, qtype, K, N in LAYER:
-                q8 = {2560: self.q8_attn if name.startswith("attn") else self.q8_ffn,
-                      4096: self.q8_o, 9728: self.q8_h}[K]
-                out.append((name, qtype, K, N, layer[name], q8, self.y[name]))
+            segs = [(layer[n], q, N, y[n]) for n, q, K, N in LAYER[:3]]
+            out.append(Op("attn_qkv", sum(weight_bytes(q, 2560, N) for n, q, K, N in LAYER[:3])
+                          + 4 * M * (2560 + 4096 + 1024 + 1024),
+                          lambda segs=segs: qk.matmul_segments(self.x_attn, M, 2560, segs, stream)))
+            w_o = layer["attn_output"]
+            out.append(Op("attn_output", gemv_bytes(Q4, 4096, 2560, M),
+                          lambda w=w_o: qk.matmul(self.x_o, w, Q4, 4096, 2560, y["attn_output"], M, stream)))
+            g, u = layer["ffn_gate"], layer["ffn_up"]
+            out.append(Op("ffn_gate_up", 2 * weight_bytes(Q4, 2560, 9728) + 4 * M * (2560 + 9728),
+                          lambda g=g, u=u: qk.ffn_gate_up(self.x_ffn, g, u, Q4, 2560, 9728, self.h, M, stream)))
+            w_d = layer["ffn_down"]
+            out.append(Op("ffn_down", gemv_bytes(Q6, 9728, 2560, M),
+                          lambda w=w_d: qk.matmul(self.h, w, Q6, 9728, 2560, y["ffn_down"], M, stream)))
         name, qtype, K, N = LM_HEAD
-        out.append((name, qtype, K, N, self.lm_head, self.q8_attn, self.logits))
+        out.append(Op("lm_head", gemv_bytes(qtype, K, N, M),
+                      lambda: qk.matmul(self.x_attn, self.lm_head, qtype, K, N, self.logits, M, stream)))
         return out
 
     def bytes_per_step(self) -> int:
-        return sum(gemv_bytes(q, K, N, self.M) for _, q, K, N, *_ in self.launches())
+        return sum(op.nbytes for op in self.ops(None))
 
-    def record(self, stream, events=None) -> None:
-        """Enqueue one step; with `events`, bracket every mat-vec with an event pair."""
-        qk, M = self.qk, self.M
-        launches = iter(self.launches())
-
-        def gemv():
-            name, qtype, K, N, w, q8, y = next(launches)
-            if events is not None:
-                events[0].pop().record(stream)
-            qk.matmul_q8(q8, w, qtype, K, N, y, M, stream)
-            if events is not None:
-                events[1].pop().record(stream)
-
-        for _ in self.layers:
-            qk.quantize_q8(self.x_attn, M, 2560, self.q8_attn, stream)
-            gemv(), gemv(), gemv()                       # q, k, v
-            qk.quantize_q8(self.x_o, M, 4096, self.q8_o, stream)
-            gemv()                                       # attn_output
-            qk.quantize_q8(self.x_ffn, M, 2560, self.q8_ffn, stream)
-            gemv(), gemv()                               # gate, up
-            qk.silu_multiply(self.y["ffn_gate"], self.y["ffn_up"], self.h, M * 9728, stream)
-            qk.quantize_q8(self.h, M, 9728, self.q8_h, stream)
-            gemv()                                       # down
-        qk.quantize_q8(self.x_attn, M, 2560, self.q8_attn, stream)
-        gemv()                                           # lm_head
+    def record(self, stream) -> None:
+        for op in self.ops(stream):
+            op.call()
 
 
 def time_graph(qk, graph, stream, warmup: int, steps: int) -> float:
@@ -160,30 +156,25 @@ def time_graph(qk, graph, stream, warmup: int, steps: int) -> float:
     return ms / steps
 
 
-def kernel_roofline(qk, sweep: DecodeSweep, stream, passes: int = 3):
-    """Per-launch HIP-event durations of every mat-vec of a step, per kernel family."""
-    launches = sweep.launches()
-    per_family: dict[str, dict] = {}
-    for _ in range(passes):
-        starts = [qk.Event() for _ in launches]
-        ends = [qk.Event() for _ in launches]
-        sweep.record(stream, events=(list(reversed(starts)), list(reversed(ends))))
-        stream.synchronize()
-        for (name, qtype, K, N, *_), a, b in zip(launches, starts, ends):
-            fam = per_family.setdefault(kernel_family(qtype, K), {"ms": 0.0, "bytes": 0, "launches": 0})
-            fam["ms"] += a.elapsed_ms(b)
-            fam["bytes"] += gemv_bytes(qtype, K, N, sweep.M)
-            fam["launches"] += 1
-        for e in starts + ends:
-            e.destroy()
+def kernel_roofline(qk, sweep: DecodeSweep, stream, replays: int = 10):
+    """Per kernel family: its launches of one step captured back to back in a
+    graph, replayed between two HIP events on the launch stream; the average
+    launch duration includes the back-to-back dispatch cost, as rocprof's does."""
+    families: dict[str, list] = {}
+    for op in sweep.ops(stream):
+        families.setdefault(op.family, []).append(op)
     out = {}
-    for fam, d in per_family.items():
-        avg_us = 1000.0 * d["ms"] / d["launches"]
-        avg_bytes = d["bytes"] / d["launches"]
+    for fam, ops in families.items():
+        graph = qk.Graph.capture(stream, lambda ops=ops: [op.call() for op in ops])
+        reps = max(replays, 40 // len(ops))
+        ms = time_graph(qk, graph, stream, 2, reps)
+        graph.destroy()
+        avg_us = 1000.0 * ms / len(ops)
+        avg_bytes = sum(op.nbytes for op in ops) / len(ops)
         gbs = avg_bytes / (avg_us * 1e3)
-        out[fam] = {"launches_per_step": d["launches"] // passes, "avg_us": round(avg_us, 3),
-                    "avg_bytes": int(avg_bytes), "GB/s": round(gbs, 1),
-                    "frac": round(gbs / PEAK_HBM_GBS, 4), "total_us_per_step": round(avg_us * d["launches"] / passes, 1)}
+        out[fam] = {"launches_per_step": len(ops), "avg_us": round(avg_us, 3), "avg_bytes": int(avg_bytes),
+                    "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+                    "total_us_per_step": round(avg_us * len(ops), 1)}
     return out
 
 
@@ -290,7 +281,7 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic",
         "config": {"workload": "Qwen3-4B Q4_K_M decode projection sweep, M=1: 36 x (q,k,v,o,gate,up,down) "
-                               "+ lm_head 151936x2560 Q6_K, Q8 activations, graph-replayed",
+                               "+ lm_head 151936x2560 Q6_K, Q8 activations, 4 launches/layer, graph-replayed",
                    "tokens_per_s": round(1e3 / ms, 2), "bytes_per_step": bytes_step,
                    "frac_of_peak_hbm": round(gbs / PEAK_HBM_GBS, 4), "eager_ms_per_step": round(eager_ms, 3),
                    "device": info["name"], "arch": info["arch"]},

@@ -50,6 +50,15 @@ typedef struct qk_q8_block {
     int32_t neg32_sum_hi;
 } qk_q8_block;
 
+/* One weight matrix of a multi-segment mat-vec: N rows of `type` superblocks,
+ * output y [M x N]. */
+typedef struct qk_segment {
+    const void *w;
+    int type;
+    int64_t N;
+    float *y;
+} qk_segment;
+
 /* Message of the last failing call on this thread ("" if none). */
 const char *qk_last_error(void);
 /* Library version: major*10000 + minor*100 + patch. */
@@ -59,8 +68,8 @@ int qk_version(void);
  * Dequantize-matmul (the hot path).
  * ------------------------------------------------------------------------- */
 
-/* y[M x N] = Q8(x)[M x K] . W^T, allocating its workspace stream-ordered for
- * the duration of the call. Replaces kernels::matmul
+/* y[M x N] = Q8(x)[M x K] . W^T in one launch per 8 activation rows (the Q8
+ * quantisation runs inside the kernel; nothing is allocated). Replaces kernels::matmul
  * (include/Kernels.hpp:57-61, src/cuda/matmul.cu:130-165). Validation as the
  * reference: type must be Q4_K or Q6_K (else QK_ERR_UNSUPPORTED_TYPE),
  * K > 0, K % 256 == 0, N > 0 (else QK_ERR_INVALID_ARGUMENT); M == 0 returns
@@ -68,12 +77,13 @@ int qk_version(void);
 int qk_matmul(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
               int64_t M, qk_stream_t stream);
 
-/* Workspace bytes qk_matmul_ws needs for this shape (0 when M == 0). */
+/* Workspace bytes qk_matmul_ws needs for this shape (0: the current kernels
+ * need none). */
 size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M);
 
 /* qk_matmul with a caller-owned device workspace of at least
- * qk_matmul_workspace_size() bytes, 256-byte aligned. Allocates nothing, so it
- * can be captured into a graph. Same semantics as qk_matmul otherwise. */
+ * qk_matmul_workspace_size() bytes (may be NULL when that is 0). Same
+ * semantics as qk_matmul. */
 int qk_matmul_ws(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
                  int64_t M, void *workspace, size_t workspace_bytes, qk_stream_t stream);
 
@@ -86,6 +96,19 @@ int qk_quantize_q8(const float *x, int64_t M, int64_t K, qk_q8_block *q8,
  * Replaces project<Q4_K/Q6_K> of src/cuda/matmul.cu:86-125. */
 int qk_matmul_q8(const qk_q8_block *q8, const void *w, int type, int64_t K, int64_t N,
                  float *y, int64_t M, qk_stream_t stream);
+
+/* Several projections of the same input in one launch: segments[j].y =
+ * Q8(x) . W_j^T for j < count (count <= 4; Q4_K and Q6_K may be mixed, all of
+ * width K). Replaces the back-to-back kernels::matmul calls on one input,
+ * e.g. attn q/k/v (src/Engine.cpp:83-85). Validation per segment as qk_matmul. */
+int qk_matmul_segments(const float *x, int64_t M, int64_t K, const qk_segment *segments,
+                       int count, qk_stream_t stream);
+
+/* h[M x N] = SiLU(Q8(x) . gate^T) * (Q8(x) . up^T) in one launch, gate and up
+ * both `type` with K columns and N rows. Replaces matmul(gate), matmul(up),
+ * silu_multiply (src/Engine.cpp:98-100, src/cuda/silu_multiply.cu:6-12). */
+int qk_ffn_gate_up(const float *x, const void *gate, const void *up, int type, int64_t K,
+                   int64_t N, float *h, int64_t M, qk_stream_t stream);
 
 /* Dequantize `rows` rows of K weights (row stride row_bytes) to fp32
  * out[rows x K], bit-identical to the formulas of src/cuda/embedding.cu:6-59.
@@ -131,9 +154,8 @@ int qk_event_elapsed_ms(float *ms, qk_event_t start, qk_event_t end);
 
 /* ---------------------------------------------------------------------------
  * Graph capture of a launch sequence on a non-null stream, replayed with one
- * call (the reference lists CUDA Graphs as future work, README.md:42). Only
- * qk_quantize_q8, qk_matmul_q8, qk_matmul_ws and qk_silu_multiply may be
- * captured: they allocate nothing and record no memset.
+ * call (the reference lists CUDA Graphs as future work, README.md:42). Every
+ * compute entry point may be captured: none allocates or records a memset.
  * ------------------------------------------------------------------------- */
 int qk_stream_begin_capture(qk_stream_t stream);
 /* Ends the capture and instantiates it; *graph owns the executable graph. */

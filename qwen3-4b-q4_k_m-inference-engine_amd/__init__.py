@@ -45,6 +45,13 @@ _size = ctypes.c_size_t
 _int = ctypes.c_int
 _float = ctypes.c_float
 
+class Segment(ctypes.Structure):
+    """qk_segment: one weight matrix of a multi-segment mat-vec."""
+
+    _fields_ = [("w", ctypes.c_void_p), ("type", ctypes.c_int), ("N", ctypes.c_int64),
+                ("y", ctypes.c_void_p)]
+
+
 # name -> argument types (every function returns int status unless listed in _RESTYPES)
 _SIGNATURES = {
     "qk_last_error": [],
@@ -55,6 +62,9 @@ _SIGNATURES = {
                      _c_void_p],
     "qk_quantize_q8": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "qk_matmul_q8": [_c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _i64, _c_void_p],
+    "qk_matmul_segments": [_c_void_p, _i64, _i64, ctypes.POINTER(Segment), _int, _c_void_p],
+    "qk_ffn_gate_up": [_c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _i64,
+                       _c_void_p],
     "qk_dequantize_rows": [_c_void_p, _c_void_p, _i64, _i64, _size, _int, _c_void_p],
     "qk_silu_multiply": [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
     "qk_malloc": [ctypes.POINTER(_c_void_p), _size],
@@ -306,6 +316,18 @@ def matmul(x, w, qtype: int, K: int, N: int, y, M: int, stream=None, y_offset: i
     """y[M x N] = Q8(x)[M x K] . W^T  (qk_matmul; kernels::matmul)."""
     check(load().qk_matmul(_ptr(x), _ptr(w), qtype, K, N, _ptr(y, y_offset), M,
                            _stream_ptr(stream)))
+
+
+def matmul_segments(x, M: int, K: int, segments, stream=None) -> None:
+    """segments: [(w, qtype, N, y), ...] (qk_matmul_segments; q/k/v in one launch)."""
+    arr = (Segment * len(segments))(*[Segment(_ptr(w), qtype, N, _ptr(y)) for w, qtype, N, y in segments])
+    check(load().qk_matmul_segments(_ptr(x), M, K, arr, len(segments), _stream_ptr(stream)))
+
+
+def ffn_gate_up(x, gate, up, qtype: int, K: int, N: int, h, M: int, stream=None) -> None:
+    """h = SiLU(x . gate^T) * (x . up^T) (qk_ffn_gate_up)."""
+    check(load().qk_ffn_gate_up(_ptr(x), _ptr(gate), _ptr(up), qtype, K, N, _ptr(h), M,
+                                _stream_ptr(stream)))
 
 
 def matmul_workspace_size(qtype: int, K: int, N: int, M: int) -> int:

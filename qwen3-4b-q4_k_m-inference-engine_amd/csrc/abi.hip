@@ -7,6 +7,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <string>
 
 #include "qk_abi.h"
@@ -37,27 +38,71 @@ size_t superblock_bytes(int type) {
 int validate_matmul(int type, int64_t K, int64_t N, int64_t M) {
   if (!supported_type(type))
     return fail(QK_ERR_UNSUPPORTED_TYPE, "matmul supports Q4_K and Q6_K weights only");
-  if (K <= 0 || K % 256 != 0 || N <= 0 || N > (int64_t{1} << 31) - 8)
+  if (K <= 0 || K % 256 != 0 || N <= 0 || N > (int64_t{1} << 31) - 64)
     return fail(QK_ERR_INVALID_ARGUMENT, "Invalid matmul weight dimensions");
-  if (M < 0 || M > 65535)
-    return fail(QK_ERR_INVALID_ARGUMENT, "matmul rows must be in [0, 65535]");
+  if (M < 0) return fail(QK_ERR_INVALID_ARGUMENT, "matmul rows must be >= 0");
   return QK_OK;
-}
-
-size_t q8_bytes(int64_t M, int64_t K) {
-  return static_cast<size_t>(M) * static_cast<size_t>(K / 32) * sizeof(qk_q8_block);
 }
 
 hipStream_t as_stream(qk_stream_t s) { return static_cast<hipStream_t>(s); }
 
-int run_matmul(const float* x, const void* w, int type, int64_t K, int64_t N, float* y,
-               int64_t M, void* workspace, hipStream_t stream) {
-  auto* q8 = static_cast<qk_q8_block*>(workspace);
-  hipError_t error = qk::launch_quantize_q8(x, M, K, q8, stream);
-  if (error != hipSuccess) return hip_fail(error, "quantize launch failed");
-  error = qk::launch_gemv(q8, w, type, K, N, y, M, stream);
-  if (error != hipSuccess) return hip_fail(error, "matmul launch failed");
+int validate_segment(const qk_segment& sg) {
+  if (!supported_type(sg.type))
+    return fail(QK_ERR_UNSUPPORTED_TYPE, "matmul supports Q4_K and Q6_K weights only");
+  if (sg.N <= 0 || sg.N > (int64_t{1} << 31) - 64)
+    return fail(QK_ERR_INVALID_ARGUMENT, "Invalid matmul weight dimensions");
   return QK_OK;
+}
+
+// The kernels read Q4_K superblocks in aligned 16-byte pieces and Q6_K ones
+// from the dword boundary at or below each field, so the tensor base must be
+// 16- (Q4_K) or 4-byte (Q6_K) aligned; device allocations and GGUF tensor
+// data (32-byte alignment) always are.
+int validate_weight_pointer(const void* w, int type) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(w);
+  if (a % (type == QK_TYPE_Q4_K ? 16 : 4) != 0)
+    return fail(QK_ERR_INVALID_ARGUMENT,
+                type == QK_TYPE_Q4_K ? "Q4_K weights must be 16-byte aligned"
+                                     : "Q6_K weights must be 4-byte aligned");
+  return QK_OK;
+}
+
+// Runs the streaming mat-vec over M activation rows, up to 8 per launch (fewer
+// when K is so wide that 8 rows of Q8 blocks do not fit in LDS).
+int run_matvec(qk::MatvecParams base, int64_t M, int64_t K, int mode, hipStream_t stream) {
+  const int chunk = qk::matvec_rows_per_launch(K);
+  if (chunk <= 0) return fail(QK_ERR_INVALID_ARGUMENT, "matmul width K exceeds the LDS capacity");
+  base.K = static_cast<int32_t>(K);
+  base.S = static_cast<int32_t>(K / 256);
+  for (int64_t m0 = 0; m0 < M; m0 += chunk) {
+    qk::MatvecParams p = base;
+    p.M = static_cast<int32_t>(std::min<int64_t>(chunk, M - m0));
+    if (p.x) p.x += m0 * K;
+    else p.q8 += m0 * (K / 32);
+    for (int j = 0; j < p.nseg; ++j)
+      if (p.seg[j].y) p.seg[j].y += m0 * p.seg[j].rows;
+    if (p.h) p.h += m0 * p.seg[0].rows;
+    const hipError_t error = qk::launch_matvec(p, mode, stream);
+    if (error != hipSuccess) return hip_fail(error, "matmul launch failed");
+  }
+  return QK_OK;
+}
+
+qk::MatvecParams params_for(const float* x, const qk_q8_block* q8) {
+  qk::MatvecParams p{};
+  p.x = x;
+  p.q8 = q8;
+  return p;
+}
+
+int run_single(const float* x, const qk_q8_block* q8, const void* w, int type, int64_t K,
+               int64_t N, float* y, int64_t M, hipStream_t stream) {
+  const int status = validate_weight_pointer(w, type);
+  if (status != QK_OK) return status;
+  qk::MatvecParams p = params_for(x, q8);
+  p.nseg = 1;
+  p.seg[0] = {static_cast<const uint8_t*>(w), y, static_cast<int32_t>(N), type, 0, 0};
+  return run_matvec(p, M, K, 0, stream);
 }
 
 }  // namespace
@@ -66,12 +111,9 @@ extern "C" {
 
 const char* qk_last_error(void) { return g_last_error.c_str(); }
 
-int qk_version(void) { return 100; }
+int qk_version(void) { return 200; }
 
-size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M) {
-  if (!supported_type(type) || K <= 0 || K % 256 != 0 || N <= 0 || M <= 0) return 0;
-  return q8_bytes(M, K);
-}
+size_t qk_matmul_workspace_size(int, int64_t, int64_t, int64_t) { return 0; }
 
 int qk_matmul(const float* x, const void* w, int type, int64_t K, int64_t N, float* y, int64_t M,
               qk_stream_t stream) {
@@ -79,29 +121,14 @@ int qk_matmul(const float* x, const void* w, int type, int64_t K, int64_t N, flo
   if (status != QK_OK) return status;
   if (M == 0) return QK_OK;
   if (!x || !w || !y) return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
-  const hipStream_t s = as_stream(stream);
-  void* workspace = nullptr;
-  hipError_t error = hipMallocAsync(&workspace, q8_bytes(M, K), s);
-  if (error != hipSuccess) return hip_fail(error, "hipMallocAsync failed");
-  const int result = run_matmul(x, w, type, K, N, y, M, workspace, s);
-  error = hipFreeAsync(workspace, s);
-  if (result != QK_OK) return result;
-  if (error != hipSuccess) return hip_fail(error, "hipFreeAsync failed");
-  return QK_OK;
+  return run_single(x, nullptr, w, type, K, N, y, M, as_stream(stream));
 }
 
 int qk_matmul_ws(const float* x, const void* w, int type, int64_t K, int64_t N, float* y,
                  int64_t M, void* workspace, size_t workspace_bytes, qk_stream_t stream) {
-  const int status = validate_matmul(type, K, N, M);
-  if (status != QK_OK) return status;
-  if (M == 0) return QK_OK;
-  if (!x || !w || !y || !workspace)
-    return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
-  if (workspace_bytes < q8_bytes(M, K))
-    return fail(QK_ERR_INVALID_ARGUMENT, "matmul workspace is smaller than qk_matmul_workspace_size");
-  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
-    return fail(QK_ERR_INVALID_ARGUMENT, "matmul workspace must be 256-byte aligned");
-  return run_matmul(x, w, type, K, N, y, M, workspace, as_stream(stream));
+  (void)workspace;
+  (void)workspace_bytes;
+  return qk_matmul(x, w, type, K, N, y, M, stream);
 }
 
 int qk_quantize_q8(const float* x, int64_t M, int64_t K, qk_q8_block* q8, qk_stream_t stream) {
@@ -123,8 +150,50 @@ int qk_matmul_q8(const qk_q8_block* q8, const void* w, int type, int64_t K, int6
   if (!q8 || !w || !y) return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
   if (reinterpret_cast<uintptr_t>(q8) % 16 != 0)
     return fail(QK_ERR_INVALID_ARGUMENT, "Q8 blocks must be 16-byte aligned");
-  const hipError_t error = qk::launch_gemv(q8, w, type, K, N, y, M, as_stream(stream));
-  return error == hipSuccess ? QK_OK : hip_fail(error, "matmul launch failed");
+  return run_single(nullptr, q8, w, type, K, N, y, M, as_stream(stream));
+}
+
+int qk_matmul_segments(const float* x, int64_t M, int64_t K, const qk_segment* segments, int count,
+                       qk_stream_t stream) {
+  if (count < 1 || count > qk::kMaxSegments || !segments)
+    return fail(QK_ERR_INVALID_ARGUMENT, "segment count must be in [1, 4]");
+  if (K <= 0 || K % 256 != 0) return fail(QK_ERR_INVALID_ARGUMENT, "Invalid matmul weight dimensions");
+  if (M < 0) return fail(QK_ERR_INVALID_ARGUMENT, "matmul rows must be >= 0");
+  for (int j = 0; j < count; ++j) {
+    const int status = validate_segment(segments[j]);
+    if (status != QK_OK) return status;
+  }
+  if (M == 0) return QK_OK;
+  if (!x) return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
+  qk::MatvecParams p = params_for(x, nullptr);
+  p.nseg = count;
+  for (int j = 0; j < count; ++j) {
+    if (!segments[j].w || !segments[j].y)
+      return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
+    const int status = validate_weight_pointer(segments[j].w, segments[j].type);
+    if (status != QK_OK) return status;
+    p.seg[j] = {static_cast<const uint8_t*>(segments[j].w), segments[j].y,
+                static_cast<int32_t>(segments[j].N), segments[j].type, 0, 0};
+  }
+  return run_matvec(p, M, K, 0, as_stream(stream));
+}
+
+int qk_ffn_gate_up(const float* x, const void* gate, const void* up, int type, int64_t K, int64_t N,
+                   float* h, int64_t M, qk_stream_t stream) {
+  const int status = validate_matmul(type, K, N, M);
+  if (status != QK_OK) return status;
+  if (M == 0) return QK_OK;
+  if (!x || !gate || !up || !h) return fail(QK_ERR_INVALID_ARGUMENT, "ffn pointers must be non-null");
+  for (const void* w : {gate, up}) {
+    const int status = validate_weight_pointer(w, type);
+    if (status != QK_OK) return status;
+  }
+  qk::MatvecParams p = params_for(x, nullptr);
+  p.nseg = 2;
+  p.h = h;
+  p.seg[0] = {static_cast<const uint8_t*>(gate), nullptr, static_cast<int32_t>(N), type, 0, 0};
+  p.seg[1] = {static_cast<const uint8_t*>(up), nullptr, static_cast<int32_t>(N), type, 0, 0};
+  return run_matvec(p, M, K, 1, as_stream(stream));
 }
 
 int qk_dequantize_rows(const void* packed, float* out, int64_t rows, int64_t K, size_t row_bytes,
@@ -321,7 +390,7 @@ int qk_stream_end_capture(qk_stream_t stream, qk_graph_t* graph) {
   if (error != hipSuccess) return hip_fail(error, "end capture failed");
   hipGraphExec_t exec = nullptr;
   error = hipGraphInstantiate(&exec, captured, nullptr, nullptr, 0);
-  hipGraphDestroy(captured);
+  (void)hipGraphDestroy(captured);
   if (error != hipSuccess) return hip_fail(error, "graph instantiation failed");
   *graph = exec;
   return QK_OK;

@@ -1,128 +1,144 @@
-// Q4_K / Q6_K mat-vec over raw GGUF superblocks and Q8 activation blocks.
-//
-// Replaces project<Q4_K/Q6_K> (src/cuda/matmul.cu:86-125), which runs one
-// 128-thread block per output element. Here a wave64 owns 8 weight rows:
-// lane = (row r = lane/8, block c = lane%8), so the 8 lanes of a row cover the
-// 8 Q8 blocks (32 weights each) of a superblock and every wave-wide load
-// reads 8 whole superblocks (Q4_K: one 128-byte line of qs per row). The
-// KSPLIT waves of a workgroup split the superblocks of those 8 rows; each
-// wave issues the loads of UNROLL superblocks before it consumes any, lanes
-// reduce with DPP and waves through LDS. Activations enter as Q8 blocks read
-// through L1/L2; the weight stream is the HBM traffic.
-#include "qk_device.hpp"
-#include "qk_launch.hpp"
+// Host launcher of the streaming mat-vec (kernels in gemv_kernel.hpp,
+// instantiated per activation-row count in gemv_m{1,2,4,8}.hip): picks the
+// row unit and unroll for the shape, sizes a persistent grid from the
+// kernel's occupancy so every wave gets the same number of row units.
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "gemv_kernel.hpp"
 
 namespace qk {
+
+MatvecKernel matvec_kernel_m1(int lpr, int u, int mode, int type);
+MatvecKernel matvec_kernel_m2(int lpr, int u, int mode, int type);
+MatvecKernel matvec_kernel_m4(int lpr, int u, int mode, int type);
+MatvecKernel matvec_kernel_m8(int lpr, int u, int mode, int type);
+
 namespace {
 
-template <int TYPE>
-struct WeightFrag;
-template <>
-struct WeightFrag<QK_TYPE_Q4_K> {
-  using type = Q4KFrag;
-  static constexpr int kBytes = kQ4KBytes;
-  static __device__ __forceinline__ Q4KFrag load(const uint8_t* sb, uint32_t c) {
-    return load_q4k(sb, c);
-  }
-  static __device__ __forceinline__ float dot(const Q4KFrag& w, const XFrag& x, uint32_t c) {
-    return dot_q4k(w, x, c);
-  }
-};
-template <>
-struct WeightFrag<QK_TYPE_Q6_K> {
-  using type = Q6KFrag;
-  static constexpr int kBytes = kQ6KBytes;
-  static __device__ __forceinline__ Q6KFrag load(const uint8_t* sb, uint32_t c) {
-    return load_q6k(sb, c);
-  }
-  static __device__ __forceinline__ float dot(const Q6KFrag& w, const XFrag& x, uint32_t c) {
-    return dot_q6k(w, x, c);
-  }
+struct DeviceFacts {
+  int cus = 0;
+  size_t max_lds = 0;
 };
 
-// SB: superblocks per row (0 = runtime sb_rt). Each wave visits superblocks
-// wave, wave+KSPLIT, ... in groups of UNROLL; out-of-range slots re-load the
-// row's last superblock (in bounds) and contribute 0.
-template <int TYPE, int SB, int KSPLIT, int UNROLL>
-__global__ __launch_bounds__(64 * KSPLIT) void gemv_kernel(const uint8_t* __restrict__ w,
-                                                           const qk_q8_block* __restrict__ q8,
-                                                           float* __restrict__ y, int sb_rt,
-                                                           int N) {
-  using WF = WeightFrag<TYPE>;
-  constexpr int kBytes = WF::kBytes;
-  const int S = SB > 0 ? SB : sb_rt;
-  const uint32_t lane = threadIdx.x & 63u;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const uint32_t r = lane >> 3;
-  const uint32_t c = lane & 7u;
-  const int row_raw = static_cast<int>(blockIdx.x) * 8 + static_cast<int>(r);
-  const int row = row_raw < N ? row_raw : N - 1;  // tail rows re-read the last row
-  const int64_t m = blockIdx.y;
-  const uint8_t* wrow = w + static_cast<int64_t>(row) * S * kBytes;
-  const qk_q8_block* xrow = q8 + m * S * 8 + c;
+std::mutex g_mutex;
+std::map<int, DeviceFacts> g_devices;
+std::map<std::pair<MatvecKernel, size_t>, int> g_occupancy;
 
-  float acc = 0.0f;
-  const int slots = (S + KSPLIT - 1) / KSPLIT;  // superblocks per wave (rounded up)
-  for (int i0 = 0; i0 < slots; i0 += UNROLL) {
-    typename WF::type wf[UNROLL];
-    XFrag xf[UNROLL];
-#pragma unroll
-    for (int i = 0; i < UNROLL; ++i) {
-      int s = wave + (i0 + i) * KSPLIT;
-      s = s < S ? s : S - 1;
-      wf[i] = WF::load(wrow + s * kBytes, c);
-      xf[i] = load_x(xrow + s * 8);
-    }
-    // keep every load of the group ahead of the first dot
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < UNROLL; ++i) {
-      const float v = WF::dot(wf[i], xf[i], c);
-      acc += (wave + (i0 + i) * KSPLIT < S) ? v : 0.0f;
-    }
+hipError_t device_facts(DeviceFacts& out) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_mutex);
+  auto it = g_devices.find(device);
+  if (it == g_devices.end()) {
+    DeviceFacts f;
+    e = hipDeviceGetAttribute(&f.cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return e;
+    int lds = 0;
+    e = hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device);
+    if (e != hipSuccess) return e;
+    f.max_lds = static_cast<size_t>(lds);
+    it = g_devices.emplace(device, f).first;
   }
-  acc = octet_sum(acc);
-
-  if constexpr (KSPLIT > 1) {
-    __shared__ float partial[KSPLIT][8];
-    if (c == 0) partial[wave][r] = acc;
-    __syncthreads();
-    if (wave != 0) return;
-    acc = partial[0][r];
-#pragma unroll
-    for (int i = 1; i < KSPLIT; ++i) acc += partial[i][r];
-  }
-  if (c == 0 && row_raw < N) y[m * N + row_raw] = acc;
+  out = it->second;
+  return hipSuccess;
 }
 
-template <int TYPE, int SB, int KSPLIT, int UNROLL>
-hipError_t launch_cfg(const qk_q8_block* q8, const uint8_t* w, int sb, int64_t N, float* y,
-                      int64_t M, hipStream_t stream) {
-  const dim3 grid(static_cast<uint32_t>((N + 7) / 8), static_cast<uint32_t>(M));
-  gemv_kernel<TYPE, SB, KSPLIT, UNROLL><<<grid, dim3(64 * KSPLIT), 0, stream>>>(
-      w, q8, y, sb, static_cast<int>(N));
-  return hipGetLastError();
+hipError_t blocks_per_cu(MatvecKernel fn, size_t lds, int& out) {
+  std::lock_guard<std::mutex> lock(g_mutex);
+  const auto key = std::make_pair(fn, lds);
+  auto it = g_occupancy.find(key);
+  if (it == g_occupancy.end()) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+    int n = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 256, lds);
+    if (e != hipSuccess) return e;
+    it = g_occupancy.emplace(key, std::max(n, 1)).first;
+  }
+  out = it->second;
+  return hipSuccess;
 }
 
-template <int TYPE>
-hipError_t launch_type(const qk_q8_block* q8, const uint8_t* w, int64_t K, int64_t N, float* y,
-                       int64_t M, hipStream_t stream) {
-  const int sb = static_cast<int>(K / kQK);
-  switch (sb) {  // Qwen3-4B widths 2560, 4096, 9728: every wave loads all its slots at once
-    case 10: return launch_cfg<TYPE, 10, 5, 2>(q8, w, sb, N, y, M, stream);
-    case 16: return launch_cfg<TYPE, 16, 8, 2>(q8, w, sb, N, y, M, stream);
-    case 38: return launch_cfg<TYPE, 38, 8, 5>(q8, w, sb, N, y, M, stream);
-    default: return launch_cfg<TYPE, 0, 4, 2>(q8, w, sb, N, y, M, stream);
+// Lanes per row: the narrowest row unit that still gives at least 8 units per
+// compute unit (so every CU streams from several waves), then for 64 lanes the
+// unroll depth that wastes fewer superblock slots.
+void choose_shape(int S, int64_t rows_total, int cus, int& lpr, int& u) {
+  lpr = 64;
+  for (int cand : {8, 16, 32, 64}) {
+    if (rows_total / (64 / cand) >= 8 * static_cast<int64_t>(cus)) {
+      lpr = cand;
+      break;
+    }
+  }
+  u = lpr == 32 ? 3 : 5;
+  if (lpr == 64) {
+    auto waste = [&](int uu) { return (S + 8 * uu - 1) / (8 * uu) * (8 * uu) - S; };
+    u = waste(5) <= waste(2) ? 5 : 2;
+  }
+}
+
+MatvecKernel pick_kernel(int mt, int lpr, int u, int mode, int type) {
+  switch (mt) {
+    case 1: return matvec_kernel_m1(lpr, u, mode, type);
+    case 2: return matvec_kernel_m2(lpr, u, mode, type);
+    case 4: return matvec_kernel_m4(lpr, u, mode, type);
+    default: return matvec_kernel_m8(lpr, u, mode, type);
   }
 }
 
 }  // namespace
 
-hipError_t launch_gemv(const qk_q8_block* q8, const void* w, int type, int64_t K, int64_t N,
-                       float* y, int64_t M, hipStream_t stream) {
-  const auto* bytes = static_cast<const uint8_t*>(w);
-  if (type == QK_TYPE_Q4_K) return launch_type<QK_TYPE_Q4_K>(q8, bytes, K, N, y, M, stream);
-  return launch_type<QK_TYPE_Q6_K>(q8, bytes, K, N, y, M, stream);
+int matvec_rows_per_launch(int64_t K) {
+  DeviceFacts dev;
+  if (device_facts(dev) != hipSuccess) return 0;
+  const size_t per_row = static_cast<size_t>(K / 32) * sizeof(qk_q8_block);
+  for (int rows : {8, 4, 2, 1})
+    if (per_row * rows <= dev.max_lds) return rows;
+  return 0;
+}
+
+hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
+  DeviceFacts dev;
+  hipError_t e = device_facts(dev);
+  if (e != hipSuccess) return e;
+  const int M = p.M;
+  const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const size_t lds = static_cast<size_t>(mt) * static_cast<size_t>(p.K / 32) * sizeof(qk_q8_block);
+  if (lds > dev.max_lds) return hipErrorInvalidValue;
+  int64_t rows_total = 0;
+  for (int j = 0; j < (mode == 0 ? p.nseg : 1); ++j) rows_total += p.seg[j].rows;
+  int lpr = 8, u = 5;
+  choose_shape(p.S, rows_total, dev.cus, lpr, u);
+  int type = p.seg[0].type;
+  for (int j = 1; j < p.nseg; ++j)
+    if (p.seg[j].type != type) type = 0;
+  const int rpu = 64 / lpr;
+  int units = 0;
+  for (int j = 0; j < p.nseg; ++j) {
+    p.seg[j].unit_begin = units;
+    if (mode == 0 || j == 0) units += (p.seg[j].rows + rpu - 1) / rpu;
+    else p.seg[j].unit_begin = 0;
+  }
+  if (mode == 1) p.nseg = 1;  // units index gate rows; up is read alongside
+  p.units = units;
+  const MatvecKernel fn = pick_kernel(mt, lpr, u, mode, type);
+  if (!fn) return hipErrorInvalidValue;
+  int per_cu = 1;
+  e = blocks_per_cu(fn, lds, per_cu);
+  if (e != hipSuccess) return e;
+  // as many waves as fit, but every wave gets the same number of units
+  const int64_t max_workers = static_cast<int64_t>(dev.cus) * per_cu * 4;
+  const int64_t per_worker = (units + max_workers - 1) / max_workers;
+  const int64_t workers = (units + per_worker - 1) / per_worker;
+  const uint32_t grid = static_cast<uint32_t>((workers + 3) / 4);
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), lds, stream, p);
+  return hipGetLastError();
 }
 
 }  // namespace qk

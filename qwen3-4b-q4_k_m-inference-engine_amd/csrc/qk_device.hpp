@@ -22,6 +22,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // superblocks of a row start 2 bytes off a dword boundary. gfx950 global
 // loads accept unaligned addresses; the compiler emits one dwordx4 for these.
 typedef u32x4 u32x4_a2 __attribute__((aligned(2)));
+typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
 typedef f32x4 f32x4_a4 __attribute__((aligned(4)));
 
 static_assert(sizeof(qk_q8_block) == 48, "Q8 block is 48 bytes");
@@ -34,6 +35,12 @@ __device__ __forceinline__ u32x4 load16_a2(const void* p) {
 }
 __device__ __forceinline__ uint32_t load_u16(const void* p) {
   return *reinterpret_cast<const uint16_t*>(p);
+}
+__device__ __forceinline__ u32x4 load16_a4(const void* p) {
+  return *reinterpret_cast<const u32x4_a4*>(p);
+}
+__device__ __forceinline__ uint32_t load_u32(const void* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
 }
 
 // fp16 bits -> fp32 (exact, subnormals kept: the kernels run with fp16
@@ -92,9 +99,16 @@ struct XFrag {  // one Q8 activation block
 struct Q4KFrag {  // header + the 32 qs bytes holding sub-blocks 2j, 2j+1
   u32x4 head, q0, q1;
 };
+// Q6_K superblocks sit at 210*s, so odd ones start 2 bytes off a dword.
+// 16-byte loads at 2-byte alignment run far slower than dword-aligned ones,
+// so every Q6_K load starts on the dword boundary at or below its field
+// (36 bytes cover 32 field bytes) and v_alignbit realigns in registers.
 struct Q6KFrag {  // 32 ql bytes, 32 qh bytes, the two int8 scales, d
   u32x4 l0, l1, h0, h1;
-  uint32_t sc_pair, d_bits;
+  uint32_t l2, h2;   // the dwords after l1 / h1
+  uint32_t sc_word;  // scales[8h+2g], scales[8h+2g+1] in the low 16 bits
+  uint32_t d_bits;   // d (2-byte load: a dword could pass the superblock's end)
+  uint32_t shift;    // field misalignment in bits: 0 or 16
 };
 
 __device__ __forceinline__ XFrag load_x(const qk_q8_block* __restrict__ xb) {
@@ -119,15 +133,22 @@ __device__ __forceinline__ Q4KFrag load_q4k(const uint8_t* __restrict__ sb, uint
 __device__ __forceinline__ Q6KFrag load_q6k(const uint8_t* __restrict__ sb, uint32_t c) {
   const uint32_t h = c >> 2;
   const uint32_t g = c & 3u;
-  const uint8_t* ql = sb + 64 * h + 32 * (g & 1u);
-  const uint8_t* qh = sb + 128 + 32 * h;
+  const uint32_t mis = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sb)) & 3u;  // 0 or 2
+  const uint8_t* base = sb - mis;  // dword-aligned
+  const uint8_t* ql = base + 64 * h + 32 * (g & 1u);
+  const uint8_t* qh = base + 128 + 32 * h;
   Q6KFrag f;
-  f.l0 = load16_a2(ql);
-  f.l1 = load16_a2(ql + 16);
-  f.h0 = load16_a2(qh);
-  f.h1 = load16_a2(qh + 16);
-  f.sc_pair = load_u16(sb + 192 + 8 * h + 2 * g);
+  f.l0 = load16_a4(ql);
+  f.l1 = load16_a4(ql + 16);
+  f.l2 = load_u32(ql + 32);
+  f.h0 = load16_a4(qh);
+  f.h1 = load16_a4(qh + 16);
+  f.h2 = load_u32(qh + 32);
+  // the scale pair's dword spans at most bytes 204..209 of the superblock
+  const uint32_t sc_off = 192 + 8 * h + 2 * g + mis;  // from base
+  f.sc_word = load_u32(base + (sc_off & ~3u)) >> (8 * (sc_off & 3u));
   f.d_bits = load_u16(sb + 208);
+  f.shift = 8 * mis;
   return f;
 }
 
@@ -161,6 +182,14 @@ __device__ __forceinline__ float dot_q4k(const Q4KFrag& w, const XFrag& x, uint3
 __device__ __forceinline__ float dot_q6k(const Q6KFrag& w, const XFrag& x, uint32_t c) {
   const uint32_t g = c & 3u;
   const i32x4 rec = __builtin_bit_cast(i32x4, x.rec);
+  const uint32_t sh = w.shift;
+  auto realign = [sh](uint32_t hi, uint32_t lo) { return __builtin_amdgcn_alignbit(hi, lo, sh); };
+  const uint32_t l[8] = {realign(w.l0.y, w.l0.x), realign(w.l0.z, w.l0.y), realign(w.l0.w, w.l0.z),
+                         realign(w.l1.x, w.l0.w), realign(w.l1.y, w.l1.x), realign(w.l1.z, w.l1.y),
+                         realign(w.l1.w, w.l1.z), realign(w.l2, w.l1.w)};
+  const uint32_t q[8] = {realign(w.h0.y, w.h0.x), realign(w.h0.z, w.h0.y), realign(w.h0.w, w.h0.z),
+                         realign(w.h1.x, w.h0.w), realign(w.h1.y, w.h1.x), realign(w.h1.z, w.h1.y),
+                         realign(w.h1.w, w.h1.z), realign(w.h2, w.h1.w)};
   const uint32_t lo_shift = 4u * (g >> 1);
   // rotate so bits (2g, 2g+1) of every byte land on bits 4 and 5
   const uint32_t hi_rot = (2u * g - 4u) & 31u;
@@ -168,16 +197,16 @@ __device__ __forceinline__ float dot_q6k(const Q6KFrag& w, const XFrag& x, uint3
   auto code = [&](uint32_t l, uint32_t h) {
     return ((l >> lo_shift) & kLo) | (__builtin_amdgcn_alignbit(h, h, hi_rot) & kHi);
   };
-  int dot_lo = dot4(code(w.l0.x, w.h0.x), x.c0.x, rec.z);
-  dot_lo = dot4(code(w.l0.y, w.h0.y), x.c0.y, dot_lo);
-  dot_lo = dot4(code(w.l0.z, w.h0.z), x.c0.z, dot_lo);
-  dot_lo = dot4(code(w.l0.w, w.h0.w), x.c0.w, dot_lo);
-  int dot_hi = dot4(code(w.l1.x, w.h1.x), x.c1.x, rec.w);
-  dot_hi = dot4(code(w.l1.y, w.h1.y), x.c1.y, dot_hi);
-  dot_hi = dot4(code(w.l1.z, w.h1.z), x.c1.z, dot_hi);
-  dot_hi = dot4(code(w.l1.w, w.h1.w), x.c1.w, dot_hi);
-  const int sc0 = static_cast<int>(static_cast<int8_t>(w.sc_pair & 0xFFu));
-  const int sc1 = static_cast<int>(static_cast<int8_t>(w.sc_pair >> 8));
+  int dot_lo = dot4(code(l[0], q[0]), x.c0.x, rec.z);
+  dot_lo = dot4(code(l[1], q[1]), x.c0.y, dot_lo);
+  dot_lo = dot4(code(l[2], q[2]), x.c0.z, dot_lo);
+  dot_lo = dot4(code(l[3], q[3]), x.c0.w, dot_lo);
+  int dot_hi = dot4(code(l[4], q[4]), x.c1.x, rec.w);
+  dot_hi = dot4(code(l[5], q[5]), x.c1.y, dot_hi);
+  dot_hi = dot4(code(l[6], q[6]), x.c1.z, dot_hi);
+  dot_hi = dot4(code(l[7], q[7]), x.c1.w, dot_hi);
+  const int sc0 = static_cast<int>(static_cast<int8_t>(w.sc_word & 0xFFu));
+  const int sc1 = static_cast<int>(static_cast<int8_t>((w.sc_word >> 8) & 0xFFu));
   // |sc*dot| <= 64*16*32*127 per group, the sum < 2^24: exact in fp32.
   const int isum = __mul24(sc0, dot_lo) + __mul24(sc1, dot_hi);
   const float d = half_bits_to_float(w.d_bits);

@@ -11,11 +11,38 @@
 
 namespace qk {
 
+constexpr int kMaxSegments = 4;
+
+// One weight matrix of a mat-vec launch (rows = N, y is [M x N]).
+struct MatvecSegment {
+  const uint8_t* w;
+  float* y;
+  int32_t rows;
+  int32_t type;
+  int32_t unit_begin;  // set by launch_matvec
+  int32_t pad;
+};
+
+// Kernel arguments of the streaming mat-vec. Exactly one of x (fp32, quantised
+// in the prologue) and q8 (pre-quantised blocks) is non-null.
+struct MatvecParams {
+  const float* x;
+  const qk_q8_block* q8;
+  float* h;  // FFN mode: SiLU(gate)*up output [M x N]
+  int32_t M, K, S, units, nseg, pad;
+  MatvecSegment seg[kMaxSegments];
+};
+
+// mode 0: y_j = x . W_j^T for every segment (M <= 8);
+// mode 1: seg[0] = gate, seg[1] = up, h = SiLU(x . gate^T) * (x . up^T).
+hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream);
+
+// Activation rows one launch_matvec can take for width K (its Q8 blocks live
+// in LDS): 8, 4, 2 or 1, or 0 when even one row does not fit.
+int matvec_rows_per_launch(int64_t K);
+
 hipError_t launch_quantize_q8(const float* x, int64_t M, int64_t K, qk_q8_block* q8,
                               hipStream_t stream);
-
-hipError_t launch_gemv(const qk_q8_block* q8, const void* w, int type, int64_t K, int64_t N,
-                       float* y, int64_t M, hipStream_t stream);
 
 hipError_t launch_dequantize_rows(const void* packed, float* out, int64_t rows, int64_t K,
                                   size_t row_bytes, int type, hipStream_t stream);

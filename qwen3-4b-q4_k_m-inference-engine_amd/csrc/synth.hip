@@ -23,8 +23,14 @@ __device__ __forceinline__ float u24(uint64_t w) {
   return static_cast<float>(w >> 40) * (1.0f / 16777216.0f);
 }
 
-__device__ __forceinline__ uint32_t fp16_bits(float v) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+// fp16(u24(w) * scale) with the product rounded to fp32 first. The empty asm
+// pins the fp32 product in a register: otherwise the compiler fuses the
+// multiply into the narrowing (v_fma_mixlo_f16), which rounds once, straight
+// to fp16, and breaks fp32-level ties the other way.
+__device__ __forceinline__ uint32_t scaled_fp16_bits(uint64_t w, float scale) {
+  float product = u24(w) * scale;
+  asm volatile("" : "+v"(product));
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(product));
 }
 
 __device__ __forceinline__ uint8_t byte_of(uint64_t w, uint32_t i) {
@@ -42,7 +48,7 @@ __global__ __launch_bounds__(256) void synth_q4k_kernel(uint8_t* __restrict__ ou
     uint8_t v;
     if (j < 4) {
       const float scale = j < 2 ? dmax : dminmax;
-      const uint32_t h = fp16_bits(u24(word_at(seed, base + (j >> 1))) * scale);
+      const uint32_t h = scaled_fp16_bits(word_at(seed, base + (j >> 1)), scale);
       v = static_cast<uint8_t>(h >> (8 * (j & 1u)));
     } else if (j < 16) {
       const uint32_t t = j - 4;
@@ -70,7 +76,7 @@ __global__ __launch_bounds__(256) void synth_q6k_kernel(uint8_t* __restrict__ ou
       const int raw = byte_of(word_at(seed, base + 24 + t / 8), t % 8) & 127;
       v = static_cast<uint8_t>(static_cast<int8_t>(raw - 64));
     } else {
-      const uint32_t h = fp16_bits(u24(word_at(seed, base + 26)) * dmax);
+      const uint32_t h = scaled_fp16_bits(word_at(seed, base + 26), dmax);
       v = static_cast<uint8_t>(h >> (8 * (j - 208)));
     }
     out[i] = v;

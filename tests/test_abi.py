@@ -55,7 +55,6 @@ def test_version_and_last_error_start_clean(qk):
     (12, 2560, 0, 1, 1),        # N = 0
     (14, 2560, -3, 1, 1),       # N < 0
     (12, 2560, 8, -1, 1),       # negative rows
-    (12, 2560, 8, 70000, 1),    # rows beyond the launch grid
 ])
 def test_matmul_validation_matches_reference(qk, qtype, K, N, M, code):
     lib = qk.load()
@@ -81,12 +80,17 @@ def test_other_validation(qk):
     assert lib.qk_dequantize_rows(None, None, 1, 2560, 1000, 12, None) == 1  # stride < row
     assert lib.qk_matmul(None, None, 12, 2560, 8, None, 1, None) == 1      # null pointers
     assert lib.qk_quantize_q8(None, 1, 100, None, None) == 1
-    assert lib.qk_matmul_workspace_size(12, 2560, 8, 3) == 3 * 80 * 48
-    assert lib.qk_matmul_workspace_size(12, 2560, 8, 0) == 0
-    assert lib.qk_matmul_workspace_size(13, 2560, 8, 1) == 0
-    ws = ctypes.c_void_p(256)
-    assert lib.qk_matmul_ws(ctypes.c_void_p(16), ctypes.c_void_p(16), 12, 2560, 8,
-                            ctypes.c_void_p(16), 1, ws, 10, None) == 1  # workspace too small
+    assert lib.qk_matmul_workspace_size(12, 2560, 8, 3) == 0  # Q8 runs inside the kernel
+    assert lib.qk_matmul_ws(None, None, 12, 2560, 8, None, 1, None, 0, None) == 1
+    seg = (qk.Segment * 2)(qk.Segment(16, 12, 8, 16), qk.Segment(16, 13, 8, 16))
+    assert lib.qk_matmul_segments(ctypes.c_void_p(16), 1, 2560, seg, 2, None) == 2
+    assert lib.qk_matmul_segments(ctypes.c_void_p(16), 1, 2560, seg, 0, None) == 1
+    assert lib.qk_matmul_segments(ctypes.c_void_p(16), 1, 2500, seg, 1, None) == 1
+    assert lib.qk_matmul_segments(None, 0, 2560, seg, 1, None) == 0
+    assert lib.qk_ffn_gate_up(None, None, None, 13, 2560, 8, None, 1, None) == 2
+    assert lib.qk_ffn_gate_up(None, None, None, 12, 2560, 0, None, 1, None) == 1
+    assert lib.qk_ffn_gate_up(None, None, None, 12, 2560, 8, None, 0, None) == 0
+    assert lib.qk_ffn_gate_up(None, None, None, 12, 2560, 8, None, 1, None) == 1  # null pointers
 
 
 def test_cpp_host_layer_validation():
