@@ -178,6 +178,29 @@ def kernel_roofline(qk, sweep: DecodeSweep, stream, replays: int = 10):
     return out
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_decode_sweep_m1.json"
+COPY_BYTES = 256 << 20
+
+
+def reference_copy(qk, stream) -> None:
+    """A device-to-device copy of COPY_BYTES: the known-size kernel against which
+    the FETCH_SIZE / WRITE_SIZE counters of a --pmc run of this script are scaled."""
+    src, dst = qk.DeviceBuffer(COPY_BYTES), qk.DeviceBuffer(COPY_BYTES)
+    qk.check(qk.load().qk_memcpy_d2d_async(dst.ptr, src.ptr, COPY_BYTES, stream.ptr))
+    stream.synchronize()
+    src.free()
+    dst.free()
+
+
+def measured_traffic(family: str):
+    """HBM bytes per launch of `family` from the committed counter runs, or None."""
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+        return data["families"][family]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(qk, sweep: DecodeSweep, budget_s: float):
     """The CPU oracle (OpenMP, double accumulation) on a bounded sample: the
     projections of layer 0, repeated until ~budget_s of CPU work."""
@@ -251,6 +274,7 @@ def main() -> int:
     stream.synchronize()
     eager_ms = (time.perf_counter() - e0) * 1e3
 
+    reference_copy(qk, stream)
     graph = qk.Graph.capture(stream, lambda: sweep.record(stream))
     ms = time_graph(qk, graph, stream, args.warmup, args.steps)
     bytes_step = sweep.bytes_per_step()
@@ -263,7 +287,7 @@ def main() -> int:
         dominant = max(kernels, key=lambda k: kernels[k]["total_us_per_step"])
         d = kernels[dominant]
         roofline = {"bound": "hbm", "achieved": d["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": d["frac"], "traffic": None, "kernel": dominant,
+                    "frac": d["frac"], "traffic": measured_traffic(dominant), "kernel": dominant,
                     "avg_launch_us": d["avg_us"], "avg_bytes_per_launch": d["avg_bytes"]}
         log(f"kernels: {json.dumps(kernels)}")
 

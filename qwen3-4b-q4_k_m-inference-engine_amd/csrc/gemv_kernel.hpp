@@ -101,26 +101,68 @@ __device__ __forceinline__ void quantize_group(const float (&v)[8], qk_q8_block*
   }
 }
 
-// fp32 x[M x K] -> Q8 blocks in LDS, laid out [MT][K/32]; rows m >= M are zero.
+// The prologue quantises fp32 x[M x K] into LDS Q8 blocks [MT][K/32] (rows
+// m >= M are zero), 8 activations per task, tasks strided over the 256
+// threads. The loads of a thread's first kStaged tasks are issued before the
+// weight prefetch (global loads complete in issue order, so activations
+// loaded after the prefetch would wait for all of it); further tasks load
+// and quantise afterwards.
 template <int MT>
-__device__ void quantize_into_lds(const float* __restrict__ x, int M, int K,
-                                  qk_q8_block* __restrict__ lds) {
-  const int groups = K / 8;  // multiple of 32, so quads never straddle the loop bound
-  for (int t = threadIdx.x; t < MT * groups; t += blockDim.x) {
-    const int m = t / groups;
-    const int g = t - m * groups;
-    float v[8];
-    if (m < M) {
-      const float* p = x + static_cast<int64_t>(m) * K + 8 * g;
-      const f32x4 a = *reinterpret_cast<const f32x4_a4*>(p);
-      const f32x4 b = *reinterpret_cast<const f32x4_a4*>(p + 4);
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
+struct XStage {
+  static constexpr int kStaged = MT == 1 ? 5 : MT == 2 ? 3 : 2;
+  f32x4 a[kStaged], b[kStaged];
+};
+
+// Loads of every staged task are unconditional (indices clamped into the
+// buffer, rows m >= M selected to zero afterwards): a load under a branch
+// would make the compiler's wait-count tracking assume nothing was issued
+// after it and wait for the whole weight prefetch before the quantisation.
+template <int MT>
+__device__ __forceinline__ void load_x_group(const float* __restrict__ x, int M, int K, int t,
+                                             f32x4& a, f32x4& b) {
+  const int groups = K / 8;
+  const int m = t / groups;
+  const float* p = x + static_cast<int64_t>(min(m, M - 1)) * K + 8 * (t - m * groups);
+  a = *reinterpret_cast<const f32x4_a4*>(p);
+  b = *reinterpret_cast<const f32x4_a4*>(p + 4);
+}
+
+template <int MT>
+__device__ __forceinline__ void stage_x(const float* __restrict__ x, int M, int K, XStage<MT>& st) {
+  const int tasks = MT * (K / 8);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-    }
-    quantize_group(v, lds + m * (K / 32) + g / 4, static_cast<uint32_t>(g & 3));
+  for (int i = 0; i < XStage<MT>::kStaged; ++i) {
+    const int t = min(static_cast<int>(threadIdx.x) + 256 * i, tasks - 1);
+    load_x_group<MT>(x, M, K, t, st.a[i], st.b[i]);
+  }
+}
+
+__device__ __forceinline__ void quantize_task(f32x4 a, f32x4 b, bool zero, int t,
+                                              qk_q8_block* __restrict__ lds) {
+  if (zero) {
+    a = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    b = a;
+  }
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  // task t covers activations 8t..8t+7 of the [MT][K] stream: block t/4, quarter t%4
+  quantize_group(v, lds + t / 4, static_cast<uint32_t>(t & 3));
+}
+
+// K/8 is a multiple of 32, so the 4 lanes of a quad are always in or out together.
+template <int MT>
+__device__ void quantize_into_lds(const float* __restrict__ x, int M, int K, const XStage<MT>& st,
+                                  qk_q8_block* __restrict__ lds) {
+  const int groups = K / 8;
+  const int tasks = MT * groups;
+#pragma unroll
+  for (int i = 0; i < XStage<MT>::kStaged; ++i) {
+    const int t = static_cast<int>(threadIdx.x) + 256 * i;
+    if (t < tasks) quantize_task(st.a[i], st.b[i], t / groups >= M, t, lds);
+  }
+  for (int t = static_cast<int>(threadIdx.x) + 256 * XStage<MT>::kStaged; t < tasks; t += 256) {
+    f32x4 a, b;
+    load_x_group<MT>(x, M, K, t, a, b);
+    quantize_task(a, b, t / groups >= M, t, lds);
   }
 }
 
@@ -239,20 +281,24 @@ __global__ __launch_bounds__(256) void matvec_kernel(const MatvecParams p) {
     row = min(row_raw, p.seg[j].rows - 1);  // tail lanes re-read the last row
   };
 
-  // Issue the first chunk of this wave's first unit before the prologue, so
-  // the quantisation below runs while those loads are in flight.
+  // Activation loads first, then the first chunk of this wave's first unit,
+  // so the quantisation below runs while the weight loads are in flight.
+  XStage<MT> stage;
+  if (p.x) stage_x<MT>(p.x, p.M, p.K, stage);
+  __builtin_amdgcn_sched_barrier(0);
+  // Waves without a unit prefetch the last unit (in bounds, unused), so the
+  // loads are issued on every path.
   typename WeightFrag<kPre>::type pre[U];
   const bool prefetched = TYPE != 0 && first < p.units;
   if constexpr (TYPE != 0) {
-    if (prefetched) {
-      int j, row_raw, row;
-      unit_row(first, j, row_raw, row);
-      issue_chunk<TYPE, LPR, U>(p.seg[j].w + static_cast<int64_t>(row) * S * WeightFrag<TYPE>::kBytes,
-                                S, 0, c, pre);
-    }
+    int j, row_raw, row;
+    unit_row(min(first, p.units - 1), j, row_raw, row);
+    issue_chunk<TYPE, LPR, U>(p.seg[j].w + static_cast<int64_t>(row) * S * WeightFrag<TYPE>::kBytes,
+                              S, 0, c, pre);
   }
+  __builtin_amdgcn_sched_barrier(0);
   if (p.x)
-    quantize_into_lds<MT>(p.x, p.M, p.K, xq);
+    quantize_into_lds<MT>(p.x, p.M, p.K, stage, xq);
   else
     copy_q8_into_lds<MT>(p.q8, p.M, p.K, xq);
   __syncthreads();

@@ -106,9 +106,10 @@ struct Q4KFrag {  // header + the 32 qs bytes holding sub-blocks 2j, 2j+1
 struct Q6KFrag {  // 32 ql bytes, 32 qh bytes, the two int8 scales, d
   u32x4 l0, l1, h0, h1;
   uint32_t l2, h2;   // the dwords after l1 / h1
-  uint32_t sc_word;  // scales[8h+2g], scales[8h+2g+1] in the low 16 bits
+  uint32_t sc_word;  // dword holding scales[8h+2g], scales[8h+2g+1]
   uint32_t d_bits;   // d (2-byte load: a dword could pass the superblock's end)
   uint32_t shift;    // field misalignment in bits: 0 or 16
+  uint32_t sc_shift; // bit offset of the scale pair in sc_word: 0 or 16
 };
 
 __device__ __forceinline__ XFrag load_x(const qk_q8_block* __restrict__ xb) {
@@ -144,9 +145,12 @@ __device__ __forceinline__ Q6KFrag load_q6k(const uint8_t* __restrict__ sb, uint
   f.h0 = load16_a4(qh);
   f.h1 = load16_a4(qh + 16);
   f.h2 = load_u32(qh + 32);
-  // the scale pair's dword spans at most bytes 204..209 of the superblock
+  // The scale pair's dword spans at most bytes 204..209 of the superblock.
+  // Shifts are applied in dot_q6k: using a loaded value here would make the
+  // wave wait for the load before it can issue the next superblock's loads.
   const uint32_t sc_off = 192 + 8 * h + 2 * g + mis;  // from base
-  f.sc_word = load_u32(base + (sc_off & ~3u)) >> (8 * (sc_off & 3u));
+  f.sc_word = load_u32(base + (sc_off & ~3u));
+  f.sc_shift = 8 * (sc_off & 3u);
   f.d_bits = load_u16(sb + 208);
   f.shift = 8 * mis;
   return f;
@@ -205,8 +209,9 @@ __device__ __forceinline__ float dot_q6k(const Q6KFrag& w, const XFrag& x, uint3
   dot_hi = dot4(code(l[5], q[5]), x.c1.y, dot_hi);
   dot_hi = dot4(code(l[6], q[6]), x.c1.z, dot_hi);
   dot_hi = dot4(code(l[7], q[7]), x.c1.w, dot_hi);
-  const int sc0 = static_cast<int>(static_cast<int8_t>(w.sc_word & 0xFFu));
-  const int sc1 = static_cast<int>(static_cast<int8_t>((w.sc_word >> 8) & 0xFFu));
+  const uint32_t pair = w.sc_word >> w.sc_shift;
+  const int sc0 = static_cast<int>(static_cast<int8_t>(pair & 0xFFu));
+  const int sc1 = static_cast<int>(static_cast<int8_t>((pair >> 8) & 0xFFu));
   // |sc*dot| <= 64*16*32*127 per group, the sum < 2^24: exact in fp32.
   const int isum = __mul24(sc0, dot_lo) + __mul24(sc1, dot_hi);
   const float d = half_bits_to_float(w.d_bits);
