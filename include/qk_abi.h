@@ -68,22 +68,30 @@ int qk_version(void);
  * Dequantize-matmul (the hot path).
  * ------------------------------------------------------------------------- */
 
-/* y[M x N] = Q8(x)[M x K] . W^T in one launch per 8 activation rows (the Q8
- * quantisation runs inside the kernel; nothing is allocated). Replaces kernels::matmul
+/* y[M x N] = Q8(x)[M x K] . W^T. Replaces kernels::matmul
  * (include/Kernels.hpp:57-61, src/cuda/matmul.cu:130-165). Validation as the
  * reference: type must be Q4_K or Q6_K (else QK_ERR_UNSUPPORTED_TYPE),
  * K > 0, K % 256 == 0, N > 0 (else QK_ERR_INVALID_ARGUMENT); M == 0 returns
- * QK_OK without launching. */
+ * QK_OK without launching.
+ * M <= 8 (decode): one streaming mat-vec launch per 8 rows, Q8 quantisation
+ * inside the kernel, integer dot products as the reference; nothing is
+ * allocated. M > 8 (prefill): the activations' Q8 round trip, scaled per row
+ * by a power of two, is stored as two fp16 planes hi + lo in a stream-ordered
+ * scratch buffer (qk_matmul_workspace_size bytes, allocated and freed on
+ * `stream` like the reference's per-call workspace); an MFMA GEMM runs on
+ * weights dequantised in LDS and split the same way, summing hi*hi + hi*lo +
+ * lo*hi in fp32 (operands carry 22 significant bits). */
 int qk_matmul(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
               int64_t M, qk_stream_t stream);
 
-/* Workspace bytes qk_matmul_ws needs for this shape (0: the current kernels
- * need none). */
+/* Workspace bytes qk_matmul_ws needs for this shape: 0 for M <= 8, else
+ * M*K*4 + M*4 rounded up to 256 (0 for shapes qk_matmul rejects). */
 size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M);
 
-/* qk_matmul with a caller-owned device workspace of at least
- * qk_matmul_workspace_size() bytes (may be NULL when that is 0). Same
- * semantics as qk_matmul. */
+/* qk_matmul with a caller-owned device workspace (16-byte aligned) of at least
+ * qk_matmul_workspace_size() bytes (may be NULL when that is 0); allocates
+ * nothing, so it can be captured into a graph at any M. Same results as
+ * qk_matmul. */
 int qk_matmul_ws(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
                  int64_t M, void *workspace, size_t workspace_bytes, qk_stream_t stream);
 

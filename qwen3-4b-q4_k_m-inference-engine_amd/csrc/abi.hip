@@ -105,6 +105,43 @@ int run_single(const float* x, const qk_q8_block* q8, const void* w, int type, i
   return run_matvec(p, M, K, 0, stream);
 }
 
+// Prefill path (M > 8 rows): activation prep once, then one MFMA GEMM per
+// weight matrix. Without a caller workspace the fp16 activation scratch is
+// allocated stream-ordered for the call, as the reference allocates its Q8
+// workspace per call (src/cuda/matmul.cu:143-145).
+int run_gemm(const float* x, int64_t M, int64_t K, const qk_segment* segments, int count,
+             void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  for (int j = 0; j < count; ++j) {
+    const int status = validate_weight_pointer(segments[j].w, segments[j].type);
+    if (status != QK_OK) return status;
+    const int64_t m_tiles = (M + 127) / 128, n_tiles = (segments[j].N + 63) / 64;
+    if (M > (int64_t{1} << 31) - 128 || m_tiles * n_tiles > (int64_t{1} << 31) - 1)
+      return fail(QK_ERR_INVALID_ARGUMENT, "matmul rows x columns exceed the launch grid");
+  }
+  const size_t need = qk::gemm_workspace_bytes(M, K);
+  void* scratch = workspace;
+  if (scratch) {
+    if (workspace_bytes < need) return fail(QK_ERR_INVALID_ARGUMENT, "matmul workspace too small");
+    if (reinterpret_cast<uintptr_t>(scratch) % 16 != 0)
+      return fail(QK_ERR_INVALID_ARGUMENT, "matmul workspace must be 16-byte aligned");
+  } else {
+    const hipError_t error = hipMallocAsync(&scratch, need, stream);
+    if (error != hipSuccess) return hip_fail(error, "matmul workspace allocation failed");
+  }
+  hipError_t error = qk::launch_gemm_prep(x, M, K, scratch, stream);
+  for (int j = 0; j < count && error == hipSuccess; ++j)
+    error = qk::launch_gemm_core(scratch, segments[j].w, segments[j].type, K, segments[j].N,
+                                 segments[j].y, M, stream);
+  if (!workspace) (void)hipFreeAsync(scratch, stream);
+  return error == hipSuccess ? QK_OK : hip_fail(error, "matmul launch failed");
+}
+
+int run_gemm_single(const float* x, const void* w, int type, int64_t K, int64_t N, float* y,
+                    int64_t M, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const qk_segment segment{w, type, N, y};
+  return run_gemm(x, M, K, &segment, 1, workspace, workspace_bytes, stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -113,7 +150,10 @@ const char* qk_last_error(void) { return g_last_error.c_str(); }
 
 int qk_version(void) { return 200; }
 
-size_t qk_matmul_workspace_size(int, int64_t, int64_t, int64_t) { return 0; }
+size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M) {
+  if (!supported_type(type) || K <= 0 || K % 256 != 0 || N <= 0 || M <= qk::kGemvMaxRows) return 0;
+  return qk::gemm_workspace_bytes(M, K);
+}
 
 int qk_matmul(const float* x, const void* w, int type, int64_t K, int64_t N, float* y, int64_t M,
               qk_stream_t stream) {
@@ -121,14 +161,20 @@ int qk_matmul(const float* x, const void* w, int type, int64_t K, int64_t N, flo
   if (status != QK_OK) return status;
   if (M == 0) return QK_OK;
   if (!x || !w || !y) return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
+  if (M > qk::kGemvMaxRows)
+    return run_gemm_single(x, w, type, K, N, y, M, nullptr, 0, as_stream(stream));
   return run_single(x, nullptr, w, type, K, N, y, M, as_stream(stream));
 }
 
 int qk_matmul_ws(const float* x, const void* w, int type, int64_t K, int64_t N, float* y,
                  int64_t M, void* workspace, size_t workspace_bytes, qk_stream_t stream) {
-  (void)workspace;
-  (void)workspace_bytes;
-  return qk_matmul(x, w, type, K, N, y, M, stream);
+  const int status = validate_matmul(type, K, N, M);
+  if (status != QK_OK) return status;
+  if (M == 0) return QK_OK;
+  if (!x || !w || !y) return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
+  if (M <= qk::kGemvMaxRows) return run_single(x, nullptr, w, type, K, N, y, M, as_stream(stream));
+  if (!workspace) return fail(QK_ERR_INVALID_ARGUMENT, "matmul workspace must be non-null");
+  return run_gemm_single(x, w, type, K, N, y, M, workspace, workspace_bytes, as_stream(stream));
 }
 
 int qk_quantize_q8(const float* x, int64_t M, int64_t K, qk_q8_block* q8, qk_stream_t stream) {
@@ -165,6 +211,10 @@ int qk_matmul_segments(const float* x, int64_t M, int64_t K, const qk_segment* s
   }
   if (M == 0) return QK_OK;
   if (!x) return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
+  for (int j = 0; j < count; ++j)
+    if (!segments[j].w || !segments[j].y)
+      return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
+  if (M > qk::kGemvMaxRows) return run_gemm(x, M, K, segments, count, nullptr, 0, as_stream(stream));
   qk::MatvecParams p = params_for(x, nullptr);
   p.nseg = count;
   for (int j = 0; j < count; ++j) {

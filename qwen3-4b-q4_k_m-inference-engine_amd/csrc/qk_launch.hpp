@@ -41,6 +41,22 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream);
 // in LDS): 8, 4, 2 or 1, or 0 when even one row does not fit.
 int matvec_rows_per_launch(int64_t K);
 
+// Activation rows above which matmul runs as the MFMA GEMM instead of the mat-vec.
+constexpr int64_t kGemvMaxRows = 8;
+
+// Bytes of device scratch launch_gemm needs for M x K activations (their fp16
+// Q8 round trip), rounded up to 256.
+size_t gemm_workspace_bytes(int64_t M, int64_t K);
+
+// workspace (>= gemm_workspace_bytes(M, K), 16-byte aligned) = fp16 of the Q8
+// round trip of x[M x K].
+hipError_t launch_gemm_prep(const float* x, int64_t M, int64_t K, void* workspace,
+                            hipStream_t stream);
+
+// y[M x N] = workspace . dequant(W)^T on MFMA, fp32 accumulation.
+hipError_t launch_gemm_core(const void* workspace, const void* w, int type, int64_t K, int64_t N,
+                            float* y, int64_t M, hipStream_t stream);
+
 hipError_t launch_quantize_q8(const float* x, int64_t M, int64_t K, qk_q8_block* q8,
                               hipStream_t stream);
 

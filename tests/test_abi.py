@@ -81,6 +81,17 @@ def test_other_validation(qk):
     assert lib.qk_matmul(None, None, 12, 2560, 8, None, 1, None) == 1      # null pointers
     assert lib.qk_quantize_q8(None, 1, 100, None, None) == 1
     assert lib.qk_matmul_workspace_size(12, 2560, 8, 3) == 0  # Q8 runs inside the kernel
+    # M > 8: two fp16 planes (hi, lo) of M x K plus M row scales, rounded up to 256
+    assert lib.qk_matmul_workspace_size(12, 2560, 8, 9) == 92416  # 9*2560*4 + 36 -> 361*256
+    assert lib.qk_matmul_workspace_size(14, 256, 8, 11) == 11520  # 11*256*4 + 44 -> 45*256
+    assert lib.qk_matmul_workspace_size(14, 2500, 8, 11) == 0  # rejected shape
+    p = ctypes.c_void_p(256)
+    assert lib.qk_matmul_ws(p, p, 12, 2560, 8, p, 9, None, 0, None) == 1  # M > 8 needs scratch
+    assert b"workspace" in lib.qk_last_error()
+    assert lib.qk_matmul_ws(p, p, 12, 2560, 8, p, 9, p, 92416 - 256, None) == 1
+    assert b"too small" in lib.qk_last_error()
+    assert lib.qk_matmul_ws(p, ctypes.c_void_p(8), 12, 2560, 8, p, 9, p, 1 << 20, None) == 1
+    assert b"aligned" in lib.qk_last_error()
     assert lib.qk_matmul_ws(None, None, 12, 2560, 8, None, 1, None, 0, None) == 1
     seg = (qk.Segment * 2)(qk.Segment(16, 12, 8, 16), qk.Segment(16, 13, 8, 16))
     assert lib.qk_matmul_segments(ctypes.c_void_p(16), 1, 2560, seg, 2, None) == 2

@@ -51,13 +51,21 @@ def run_matmul(qk, w, qtype, K, N, x_host, M):
     return y.download(np.float32, M * N).reshape(M, N)
 
 
-def assert_parity(oracle, got, ref, approx_floor=0.999):
+# Above this many activation rows matmul runs the MFMA GEMM (fp16 hi + lo
+# operand splits, fp32 accumulation in another order than the mat-vec's
+# integer dots): same row-norm bar, Approx floor 0.99 instead of the floor
+# the integer path meets.
+GEMV_MAX_ROWS = 8
+GEMM_APPROX_FLOOR = 0.99
+
+
+def assert_parity(oracle, got, ref, approx_floor=0.999, integer=True):
     err = oracle.row_norm_error(got, ref)
     rate = oracle.approx_pass_rate(got, ref)
     print(f"row-norm error {err:.3e}, Approx pass rate {rate:.5f}", flush=True)
     assert err <= ROW_NORM_BAR
-    assert err <= 1e-5  # integer dots + fp32 epilogue: far inside the bar
-    assert rate >= approx_floor
+    assert err <= 1e-5  # integer dots or split-fp16 MFMA, fp32 sums: far inside the bar
+    assert rate >= (approx_floor if integer else min(approx_floor, GEMM_APPROX_FLOOR))
 
 
 # ------------------------------------------------------------- synthetic --
@@ -200,7 +208,7 @@ def test_matmul_rows_truncated_columns(gpu, oracle, qtype, K, rows):
         stream.synchronize()
         got = out.download(np.float32)
         assert got[0] == 123.0 and got[-1] == 123.0
-        assert_parity(oracle, got[1:-1], ref, approx_floor=1.0)
+        assert_parity(oracle, got[1:-1], ref, approx_floor=1.0, integer=rows <= GEMV_MAX_ROWS)
     xd.fill(0)
     gpu.matmul(xd, w, qtype, K, N, out, rows, None, y_offset=4)
     gpu.synchronize()
@@ -288,7 +296,7 @@ def test_matmul_segments_qkv(gpu, oracle, M):
     for w, (q, N), y in zip(ws, shapes, ys):
         got = y.download(np.float32).reshape(M, N)
         ref = oracle.reference_product(x, w.download(np.uint8), q, K, N)
-        assert_parity(oracle, got, ref)
+        assert_parity(oracle, got, ref, integer=M <= GEMV_MAX_ROWS)
         # a lone launch may pick another lanes-per-row split: same sums, other order
         single = run_matmul(gpu, w, q, K, N, x, M)
         assert oracle.row_norm_error(single, got.astype(np.float64)) <= 1e-6
