@@ -1,8 +1,10 @@
 // Host launcher of the streaming mat-vec (kernels in gemv_kernel.hpp,
-// instantiated per activation-row count in gemv_m{1,2,4,8}.hip): picks the
-// row unit and unroll for the shape, sizes a persistent grid from the
-// kernel's occupancy so every wave gets the same number of row units.
+// instantiated per activation-row count in gemv_m{1,2,4,8}.hip): orders the
+// segments by type, sizes the grid (one workgroup per CU, split between the
+// types of a mixed launch) and picks the lanes per row for the shape.
 #include <algorithm>
+#include <climits>
+#include <cstdint>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -11,10 +13,10 @@
 
 namespace qk {
 
-MatvecKernel matvec_kernel_m1(int lpr, int u, int mode, int type);
-MatvecKernel matvec_kernel_m2(int lpr, int u, int mode, int type);
-MatvecKernel matvec_kernel_m4(int lpr, int u, int mode, int type);
-MatvecKernel matvec_kernel_m8(int lpr, int u, int mode, int type);
+MatvecKernel matvec_kernel_m1(int lpr, int mode, int type, bool q8in);
+MatvecKernel matvec_kernel_m2(int lpr, int mode, int type, bool q8in);
+MatvecKernel matvec_kernel_m4(int lpr, int mode, int type, bool q8in);
+MatvecKernel matvec_kernel_m8(int lpr, int mode, int type, bool q8in);
 
 namespace {
 
@@ -57,7 +59,7 @@ hipError_t blocks_per_cu(MatvecKernel fn, size_t lds, int& out) {
                                        static_cast<int>(lds));
     if (e != hipSuccess) return e;
     int n = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, 256, lds);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kMatvecThreads, lds);
     if (e != hipSuccess) return e;
     it = g_occupancy.emplace(key, std::max(n, 1)).first;
   }
@@ -65,30 +67,22 @@ hipError_t blocks_per_cu(MatvecKernel fn, size_t lds, int& out) {
   return hipSuccess;
 }
 
-// Lanes per row: the narrowest row unit that still gives at least 8 units per
-// compute unit (so every CU streams from several waves), then for 64 lanes the
-// unroll depth that wastes fewer superblock slots.
-void choose_shape(int S, int64_t rows_total, int cus, int& lpr, int& u) {
-  lpr = 64;
-  for (int cand : {8, 16, 32, 64}) {
-    if (rows_total / (64 / cand) >= 8 * static_cast<int64_t>(cus)) {
-      lpr = cand;
-      break;
-    }
-  }
-  u = lpr == 32 ? 3 : 5;
-  if (lpr == 64) {
-    auto waste = [&](int uu) { return (S + 8 * uu - 1) / (8 * uu) * (8 * uu) - S; };
-    u = waste(5) <= waste(2) ? 5 : 2;
-  }
+// Iterations on the busiest wave when groups of 64/lpr rows are dealt
+// round-robin to `waves` waves, each row taking ceil(S / (lpr/4))
+// iterations (twice that for gate + up).
+int64_t wave_iterations(int64_t rows, int64_t waves, int lpr, int S, int mode) {
+  const int64_t rpg = 64 / lpr, spi = lpr / 4;
+  const int64_t groups = (rows + rpg - 1) / rpg;
+  const int64_t ipu = (S + spi - 1) / spi * (mode == 1 ? 2 : 1);
+  return (groups + waves - 1) / waves * ipu;
 }
 
-MatvecKernel pick_kernel(int mt, int lpr, int u, int mode, int type) {
+MatvecKernel pick_kernel(int mt, int lpr, int mode, int type, bool q8in) {
   switch (mt) {
-    case 1: return matvec_kernel_m1(lpr, u, mode, type);
-    case 2: return matvec_kernel_m2(lpr, u, mode, type);
-    case 4: return matvec_kernel_m4(lpr, u, mode, type);
-    default: return matvec_kernel_m8(lpr, u, mode, type);
+    case 1: return matvec_kernel_m1(lpr, mode, type, q8in);
+    case 2: return matvec_kernel_m2(lpr, mode, type, q8in);
+    case 4: return matvec_kernel_m4(lpr, mode, type, q8in);
+    default: return matvec_kernel_m8(lpr, mode, type, q8in);
   }
 }
 
@@ -111,33 +105,64 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
   const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
   const size_t lds = static_cast<size_t>(mt) * static_cast<size_t>(p.K / 32) * sizeof(qk_q8_block);
   if (lds > dev.max_lds) return hipErrorInvalidValue;
-  int64_t rows_total = 0;
-  for (int j = 0; j < (mode == 0 ? p.nseg : 1); ++j) rows_total += p.seg[j].rows;
-  int lpr = 8, u = 5;
-  choose_shape(p.S, rows_total, dev.cus, lpr, u);
-  int type = p.seg[0].type;
-  for (int j = 1; j < p.nseg; ++j)
-    if (p.seg[j].type != type) type = 0;
-  const int rpu = 64 / lpr;
-  int units = 0;
+
+  // Row space: the segments' rows back to back, Q4_K segments first (the
+  // mixed kernel gives each type its own workgroups). The FFN mode streams
+  // the gate rows; up is read alongside through seg[1].
+  if (mode == 1) p.nseg = 1;
+  std::stable_sort(p.seg, p.seg + p.nseg, [](const MatvecSegment& l, const MatvecSegment& r) {
+    return l.type == QK_TYPE_Q4_K && r.type != QK_TYPE_Q4_K;
+  });
+  int64_t rows4 = 0, rows6 = 0, begin = 0;
   for (int j = 0; j < p.nseg; ++j) {
-    p.seg[j].unit_begin = units;
-    if (mode == 0 || j == 0) units += (p.seg[j].rows + rpu - 1) / rpu;
-    else p.seg[j].unit_begin = 0;
+    p.seg[j].row_begin = static_cast<int32_t>(begin);
+    begin += p.seg[j].rows;
+    (p.seg[j].type == QK_TYPE_Q4_K ? rows4 : rows6) += p.seg[j].rows;
   }
-  if (mode == 1) p.nseg = 1;  // units index gate rows; up is read alongside
-  p.units = units;
-  const MatvecKernel fn = pick_kernel(mt, lpr, u, mode, type);
-  if (!fn) return hipErrorInvalidValue;
+  if (begin > INT32_MAX - 64) return hipErrorInvalidValue;
+  p.rows_total = static_cast<int32_t>(begin);
+  const int type = rows6 == 0 ? QK_TYPE_Q4_K : rows4 == 0 ? QK_TYPE_Q6_K : 0;
+
+  // Workgroups: one per CU (times the occupancy), never more than rows; a
+  // mixed launch splits them in proportion to each type's bytes.
+  const MatvecKernel probe = pick_kernel(mt, 8, mode, type, p.x == nullptr);
+  if (!probe) return hipErrorInvalidValue;
   int per_cu = 1;
-  e = blocks_per_cu(fn, lds, per_cu);
+  e = blocks_per_cu(probe, lds, per_cu);
   if (e != hipSuccess) return e;
-  // as many waves as fit, but every wave gets the same number of units
-  const int64_t max_workers = static_cast<int64_t>(dev.cus) * per_cu * 4;
-  const int64_t per_worker = (units + max_workers - 1) / max_workers;
-  const int64_t workers = (units + per_worker - 1) / per_worker;
-  const uint32_t grid = static_cast<uint32_t>((workers + 3) / 4);
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), lds, stream, p);
+  const int64_t grid = std::min<int64_t>(static_cast<int64_t>(dev.cus) * per_cu, begin);
+  int64_t wg4 = grid;
+  if (type == 0) {
+    if (grid < 2) return hipErrorInvalidValue;  // rows_total >= 2 here
+    const double b4 = static_cast<double>(rows4) * kQ4KBytes, b6 = static_cast<double>(rows6) * kQ6KBytes;
+    wg4 = std::clamp<int64_t>(static_cast<int64_t>(grid * b4 / (b4 + b6) + 0.5), 1, grid - 1);
+  }
+  p.split_wg = static_cast<int32_t>(wg4);
+  p.split_row = static_cast<int32_t>(rows4);
+
+  // Lanes per row: the fewest iterations (weighted by superblock bytes) on
+  // the busiest wave; ties go to the narrower row, whose reductions are shorter.
+  int lpr = 64;
+  int64_t best = INT64_MAX;
+  for (int cand : {8, 16, 32, 64}) {
+#ifdef QK_MATVEC_FORCE_LPR
+    if (cand != QK_MATVEC_FORCE_LPR) continue;
+#endif
+    int64_t cost = 0;
+    if (rows4) cost = std::max(cost, wave_iterations(rows4, wg4 * kMatvecWaves, cand, p.S, mode) * kQ4KBytes);
+    if (rows6)
+      cost = std::max(cost, wave_iterations(rows6, (type == 0 ? grid - wg4 : grid) * kMatvecWaves, cand,
+                                            p.S, mode) * kQ6KBytes);
+    if (cost < best) {
+      best = cost;
+      lpr = cand;
+    }
+  }
+  const MatvecKernel fn = pick_kernel(mt, lpr, mode, type, p.x == nullptr);
+  if (!fn) return hipErrorInvalidValue;
+  e = blocks_per_cu(fn, lds, per_cu);  // sets the kernel's dynamic LDS limit
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(grid)), dim3(kMatvecThreads), lds, stream, p);
   return hipGetLastError();
 }
 

@@ -2,17 +2,21 @@
 //
 // Replaces quantize + project<Q4_K/Q6_K> (src/cuda/matmul.cu:8-22, 86-125),
 // which run one 128-thread block per output element after a separate
-// quantize launch. Here one persistent launch does both:
-//   1. prologue: the workgroup quantises the fp32 activations into Q8 blocks
-//      in LDS (or copies caller-provided Q8 blocks), while each wave's first
-//      weight loads are already in flight;
-//   2. each wave64 is an independent worker that streams whole row units:
-//      lane = (row rr = lane / LPR, c = lane % LPR) with c -> (superblock
-//      offset c/8, Q8 block c%8), so the LPR lanes of a row cover LPR/8
-//      superblocks per iteration and every wave-wide load reads 64/LPR rows x
-//      LPR/8 whole superblocks. Loads of U iterations are issued before the
-//      first dot; lanes of a row reduce with DPP/shuffles; no barriers after
-//      the prologue.
+// quantize launch. Here one launch of 512-thread workgroups (8 waves, one
+// workgroup per CU) does both:
+//   1. prologue: every kernel argument is read in one scalar-load round; the
+//      workgroup quantises the fp32 activations into Q8 blocks in LDS (or
+//      copies caller-provided Q8 blocks) while each wave's first weight
+//      loads are already in flight;
+//   2. each wave64 is an independent worker over a flat stream of
+//      iterations: lane = (row rr = lane / LPR, c = lane % LPR) with
+//      c -> (superblock offset c/4, piece c%4), so one iteration covers
+//      64/LPR rows x LPR/4 whole superblocks. Iterations run U at a time,
+//      double buffered (the next U are loading while the current U are
+//      consumed) across row-unit boundaries; the lanes of a row reduce with
+//      DPP/shuffles when its last iteration is consumed. No barriers after
+//      the prologue, and no load is ever issued under a branch, so the
+//      compiler's wait counts stay exact.
 // Several weight segments sharing the input (attn q/k/v, src/Engine.cpp:83-85)
 // run in one launch; the FFN mode computes gate and up for the same rows and
 // writes SiLU(gate)*up (src/Engine.cpp:98-100, src/cuda/silu_multiply.cu:10).
@@ -25,30 +29,57 @@
 
 namespace qk {
 
+// Waves per workgroup, iterations per chunk (Q4_K, Q6_K) and activation
+// tasks staged per quantiser lane. The defaults are the values measured best
+// on the Qwen3-4B decode sweep (16 waves of at most 128 VGPRs, shallow
+// chunks: more waves in flight beat deeper per-wave unrolling); the macros
+// exist for tuning builds.
+#ifndef QK_MATVEC_WAVES
+#define QK_MATVEC_WAVES 16
+#endif
+#ifndef QK_MATVEC_U4
+#define QK_MATVEC_U4 2
+#endif
+#ifndef QK_MATVEC_U6
+#define QK_MATVEC_U6 1
+#endif
+#ifndef QK_MATVEC_XSTAGED
+#define QK_MATVEC_XSTAGED 2
+#endif
+constexpr int kMatvecWaves = QK_MATVEC_WAVES;
+constexpr int kMatvecThreads = 64 * kMatvecWaves;
+
+// Per-lane register image of one iteration's piece.
 template <int TYPE>
-struct WeightFrag;
-template <>
-struct WeightFrag<QK_TYPE_Q4_K> {
-  using type = Q4KFrag;
-  static constexpr int kBytes = kQ4KBytes;
-  static __device__ __forceinline__ Q4KFrag load(const uint8_t* sb, uint32_t c) {
-    return load_q4k(sb, c);
-  }
-  static __device__ __forceinline__ float dot(const Q4KFrag& w, const XFrag& x, uint32_t c) {
-    return dot_q4k(w, x, c);
-  }
+struct PieceOf {
+  using type = Q6KPiece;
 };
 template <>
-struct WeightFrag<QK_TYPE_Q6_K> {
-  using type = Q6KFrag;
-  static constexpr int kBytes = kQ6KBytes;
-  static __device__ __forceinline__ Q6KFrag load(const uint8_t* sb, uint32_t c) {
-    return load_q6k(sb, c);
-  }
-  static __device__ __forceinline__ float dot(const Q6KFrag& w, const XFrag& x, uint32_t c) {
-    return dot_q6k(w, x, c);
-  }
+struct PieceOf<QK_TYPE_Q4_K> {
+  using type = Q4KPiece;
 };
+
+template <int TYPE>
+__device__ __forceinline__ typename PieceOf<TYPE>::type load_piece(const uint8_t* sb, uint32_t pc,
+                                                                    int) {
+  if constexpr (TYPE == QK_TYPE_Q4_K) return load_q4k_piece(sb, pc);
+  else return load_q6k_piece(sb, pc);
+}
+
+template <int TYPE>
+__device__ __forceinline__ float dot_piece(const typename PieceOf<TYPE>::type& w, const XFrag& xa,
+                                           const XFrag& xb, uint32_t pc, int) {
+  if constexpr (TYPE == QK_TYPE_Q4_K) return dot_q4k_piece(w, xa, xb, pc);
+  else return dot_q6k_piece(w, xa, xb, pc);
+}
+
+// Q8 blocks a piece pairs with: Q4_K piece j -> sub-blocks 2j, 2j+1;
+// Q6_K piece p (half h, parity r) -> groups 4h+r and 4h+r+2.
+__device__ __forceinline__ int piece_block_a(uint32_t pc, int type) {
+  return type == QK_TYPE_Q4_K ? static_cast<int>(2 * pc)
+                              : static_cast<int>(4 * (pc >> 1) + (pc & 1u));
+}
+__device__ __forceinline__ int piece_block_step(int type) { return type == QK_TYPE_Q4_K ? 1 : 2; }
 
 // Q8 of one group of 8 consecutive activations per lane; the 4 lanes of a
 // quad form one 32-activation block. code = roundf(RN(x/amax)*127) with the
@@ -102,22 +133,26 @@ __device__ __forceinline__ void quantize_group(const float (&v)[8], qk_q8_block*
 }
 
 // The prologue quantises fp32 x[M x K] into LDS Q8 blocks [MT][K/32] (rows
-// m >= M are zero), 8 activations per task, tasks strided over the 256
-// threads. The loads of a thread's first kStaged tasks are issued before the
-// weight prefetch (global loads complete in issue order, so activations
-// loaded after the prefetch would wait for all of it); further tasks load
-// and quantise afterwards.
+// m >= M are zero), 8 activations per task. Only the first nq waves of the
+// workgroup (the quantiser waves) touch x: each of their lanes issues the
+// loads of up to kXStaged tasks before its weight loads and quantises them
+// while those are in flight. Global loads return in issue order per wave, so
+// the other waves' weight loads never wait behind activation loads. Tasks
+// beyond the staged ones (M > 1 with wide K) load and quantise afterwards.
+constexpr int kXStaged = QK_MATVEC_XSTAGED;
+
 template <int MT>
 struct XStage {
-  static constexpr int kStaged = MT == 1 ? 5 : MT == 2 ? 3 : 2;
-  f32x4 a[kStaged], b[kStaged];
+  f32x4 a[kXStaged], b[kXStaged];
 };
 
+// Quantiser waves for `tasks` tasks: enough for kXStaged tasks per lane.
+__device__ __forceinline__ int quantiser_waves(int tasks) {
+  return min(kMatvecWaves, (tasks + 64 * kXStaged - 1) / (64 * kXStaged));
+}
+
 // Loads of every staged task are unconditional (indices clamped into the
-// buffer, rows m >= M selected to zero afterwards): a load under a branch
-// would make the compiler's wait-count tracking assume nothing was issued
-// after it and wait for the whole weight prefetch before the quantisation.
-template <int MT>
+// buffer, rows m >= M selected to zero afterwards).
 __device__ __forceinline__ void load_x_group(const float* __restrict__ x, int M, int K, int t,
                                              f32x4& a, f32x4& b) {
   const int groups = K / 8;
@@ -127,13 +162,15 @@ __device__ __forceinline__ void load_x_group(const float* __restrict__ x, int M,
   b = *reinterpret_cast<const f32x4_a4*>(p + 4);
 }
 
+// Quantiser lane xl (threadIdx.x of a wave below nq) takes tasks xl + 64*nq*i.
 template <int MT>
-__device__ __forceinline__ void stage_x(const float* __restrict__ x, int M, int K, XStage<MT>& st) {
+__device__ __forceinline__ void stage_x(const float* __restrict__ x, int M, int K, int nq,
+                                        XStage<MT>& st) {
   const int tasks = MT * (K / 8);
 #pragma unroll
-  for (int i = 0; i < XStage<MT>::kStaged; ++i) {
-    const int t = min(static_cast<int>(threadIdx.x) + 256 * i, tasks - 1);
-    load_x_group<MT>(x, M, K, t, st.a[i], st.b[i]);
+  for (int i = 0; i < kXStaged; ++i) {
+    const int t = min(static_cast<int>(threadIdx.x) + 64 * nq * i, tasks - 1);
+    load_x_group(x, M, K, t, st.a[i], st.b[i]);
   }
 }
 
@@ -148,20 +185,22 @@ __device__ __forceinline__ void quantize_task(f32x4 a, f32x4 b, bool zero, int t
   quantize_group(v, lds + t / 4, static_cast<uint32_t>(t & 3));
 }
 
-// K/8 is a multiple of 32, so the 4 lanes of a quad are always in or out together.
+// K/8 and 64*nq are multiples of 4, so the 4 lanes of a quad are always in
+// or out together.
 template <int MT>
-__device__ void quantize_into_lds(const float* __restrict__ x, int M, int K, const XStage<MT>& st,
-                                  qk_q8_block* __restrict__ lds) {
+__device__ void quantize_into_lds(const float* __restrict__ x, int M, int K, int nq,
+                                  const XStage<MT>& st, qk_q8_block* __restrict__ lds) {
   const int groups = K / 8;
   const int tasks = MT * groups;
+  const int step = 64 * nq;
 #pragma unroll
-  for (int i = 0; i < XStage<MT>::kStaged; ++i) {
-    const int t = static_cast<int>(threadIdx.x) + 256 * i;
+  for (int i = 0; i < kXStaged; ++i) {
+    const int t = static_cast<int>(threadIdx.x) + step * i;
     if (t < tasks) quantize_task(st.a[i], st.b[i], t / groups >= M, t, lds);
   }
-  for (int t = static_cast<int>(threadIdx.x) + 256 * XStage<MT>::kStaged; t < tasks; t += 256) {
+  for (int t = static_cast<int>(threadIdx.x) + step * kXStaged; t < tasks; t += step) {
     f32x4 a, b;
-    load_x_group<MT>(x, M, K, t, a, b);
+    load_x_group(x, M, K, t, a, b);
     quantize_task(a, b, t / groups >= M, t, lds);
   }
 }
@@ -173,212 +212,297 @@ __device__ void copy_q8_into_lds(const qk_q8_block* __restrict__ q8, int M, int 
   const int per_row = (K / 32) * 3;  // 16-byte chunks
   const u32x4* src = reinterpret_cast<const u32x4*>(q8);
   u32x4* dst = reinterpret_cast<u32x4*>(lds);
-  for (int t = threadIdx.x; t < MT * per_row; t += blockDim.x) {
+  for (int t = threadIdx.x; t < MT * per_row; t += kMatvecThreads) {
     const int m = t / per_row;
     dst[t] = m < M ? src[t] : u32x4{0u, 0u, 0u, 0u};
   }
 }
 
+// Sum over the LPR lanes of each row (aligned lane groups); every lane of the
+// group receives the sum.
 template <int LPR>
 __device__ __forceinline__ float row_lanes_sum(float v) {
-  v = octet_sum(v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                             0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                             0x4E, 0xF, 0xF, false));
+  if constexpr (LPR >= 8)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               0x141, 0xF, 0xF, false));
   if constexpr (LPR >= 16) v += __shfl_xor(v, 8);
   if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
   if constexpr (LPR >= 64) v += __shfl_xor(v, 32);
   return v;
 }
 
-// Loads of one chunk of a row: U iterations of LPR/8 superblocks.
-template <int TYPE, int LPR, int U>
-__device__ __forceinline__ void issue_chunk(const uint8_t* __restrict__ wrow, int S, int s0,
-                                            uint32_t c, typename WeightFrag<TYPE>::type (&wf)[U]) {
-  using WF = WeightFrag<TYPE>;
-  constexpr int kSPI = LPR / 8;
-  const int sbo = static_cast<int>(c >> 3);
-#pragma unroll
-  for (int i = 0; i < U; ++i) {
-    const int s = min(s0 + i * kSPI + sbo, S - 1);
-    wf[i] = WF::load(wrow + s * WF::kBytes, c & 7u);
-  }
-}
+// Position of a wave's iteration in its stream: row group u (kRPU rows) and
+// iteration k within it (FFN mode: k < ipu gate, else up).
+struct Cursor {
+  int u, k;
+};
 
-// acc[m] += the chunk's dots against activation row m.
-template <int TYPE, int MT, int LPR, int U>
-__device__ __forceinline__ void consume_chunk(const typename WeightFrag<TYPE>::type (&wf)[U],
-                                              const qk_q8_block* __restrict__ xq, int S, int s0,
-                                              uint32_t c, float (&acc)[MT]) {
-  using WF = WeightFrag<TYPE>;
-  constexpr int kSPI = LPR / 8;
-  const uint32_t blk = c & 7u;
-  const int sbo = static_cast<int>(c >> 3);
-#pragma unroll
-  for (int i = 0; i < U; ++i) {
-    const int s = s0 + i * kSPI + sbo;
-    const bool valid = s < S;
-    const int sc = min(s, S - 1);
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const XFrag xf = load_x(xq + m * S * 8 + sc * 8 + static_cast<int>(blk));
-      const float v = WF::dot(wf[i], xf, blk);
-      acc[m] += valid ? v : 0.0f;
+// Kernel arguments held in scalar registers.
+struct MatvecArgs {
+  const float* x;
+  const qk_q8_block* q8;
+  float* h;
+  int M, K, S, nseg;
+  MatvecSegment sg[kMaxSegments];
+};
+
+// One weight type's share of a launch: rows [row_lo, row_hi) of the
+// concatenated segments, streamed by workgroups wg of nwg, in groups of kRPU
+// rows with each row's LPR lanes covering LPR/4 superblocks per iteration.
+template <int MT, int LPR, int U, int MODE, int TYPE, bool Q8IN>
+__device__ __forceinline__ void matvec_body(const MatvecArgs& a, int row_lo, int row_hi, int wg,
+                                            int nwg, qk_q8_block* __restrict__ xq) {
+  using Piece = typename PieceOf<TYPE>::type;
+  constexpr int kRPU = 64 / LPR;  // rows per group
+  constexpr int kSPI = LPR / 4;   // superblocks per iteration
+  constexpr int kBytes = TYPE == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes;
+  const int S = a.S, M = a.M, K = a.K, nseg = a.nseg;
+
+  const uint32_t lane = threadIdx.x & 63u;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int rr = static_cast<int>(lane) / LPR;
+  const uint32_t c = lane % LPR;
+  const uint32_t pc = c & 3u;                // piece
+  const int sbo = static_cast<int>(c >> 2);  // superblock offset within the iteration
+  // Row groups of kRPU rows are dealt round-robin: group g goes to worker
+  // g % nworkers, worker = wave*nwg + wg, so consecutive groups run on
+  // different CUs and, at any moment, the whole GPU streams one compact
+  // window of the matrix (DRAM rows stay open for many requests).
+  const int nworkers = nwg * kMatvecWaves;
+  const int wid = wave * nwg + wg;
+  const int groups_total = (row_hi - row_lo + kRPU - 1) / kRPU;
+  const int ngroups = wid < groups_total ? (groups_total - 1 - wid) / nworkers + 1 : 0;
+  const int ipu = (S + kSPI - 1) / kSPI;  // iterations per weight row
+  const int ipu_total = MODE == 1 ? 2 * ipu : ipu;
+  const int T = ngroups * ipu_total;
+  const int last_row = row_hi - 1;  // a valid row for idle loads
+  auto group_row = [&](int u) {     // first row of this worker's u-th group
+    return row_lo + (wid + u * nworkers) * kRPU;
+  };
+
+  // segment of a row, field by field (a struct picked by a runtime index
+  // would be copied to scratch memory)
+  struct Where {
+    const uint8_t* w;
+    float* y;
+    int rows, local;
+  };
+  auto locate = [&](int row, int phase) {
+    const int j = (nseg > 1 && row >= a.sg[1].row_begin) + (nseg > 2 && row >= a.sg[2].row_begin) +
+                  (nseg > 3 && row >= a.sg[3].row_begin);
+    auto pick = [j](auto f0, auto f1, auto f2, auto f3) {
+      return j == 0 ? f0 : j == 1 ? f1 : j == 2 ? f2 : f3;
+    };
+    Where o;
+    o.w = MODE == 1 && phase ? a.sg[1].w : pick(a.sg[0].w, a.sg[1].w, a.sg[2].w, a.sg[3].w);
+    o.y = pick(a.sg[0].y, a.sg[1].y, a.sg[2].y, a.sg[3].y);
+    o.rows = pick(a.sg[0].rows, a.sg[1].rows, a.sg[2].rows, a.sg[3].rows);
+    o.local = row - pick(a.sg[0].row_begin, a.sg[1].row_begin, a.sg[2].row_begin, a.sg[3].row_begin);
+    return o;
+  };
+  auto advance = [&](Cursor& cur) {
+    if (++cur.k == ipu_total) {
+      cur.k = 0;
+      ++cur.u;
     }
-  }
-}
+  };
+  // Loads of U iterations from `cur` on; iterations past the wave's stream
+  // re-read its last one (in bounds, never consumed).
+  auto issue = [&](Cursor& cur, Piece (&f)[U]) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const bool live = cur.u < ngroups;
+      const int k = live ? cur.k : ipu_total - 1;
+      const int phase = MODE == 1 && k >= ipu;
+      const int kk = phase ? k - ipu : k;
+      const int row = min(group_row(live ? cur.u : max(ngroups - 1, 0)) + rr, last_row);
+      const Where o = locate(row, phase);
+      const int s = min(kk * kSPI + sbo, S - 1);
+      f[i] = load_piece<TYPE>(o.w + (static_cast<int64_t>(o.local) * S + s) * kBytes, pc, TYPE);
+      advance(cur);
+    }
+  };
 
-// acc[m] += this lane's share of row `wrow` . x_m over all S superblocks; with
-// `have_first` the first chunk's loads were issued by the caller into wf.
-template <int TYPE, int MT, int LPR, int U>
-__device__ __forceinline__ void stream_row(const uint8_t* __restrict__ wrow,
-                                           const qk_q8_block* __restrict__ xq, int S, uint32_t c,
-                                           float (&acc)[MT], typename WeightFrag<TYPE>::type (&wf)[U],
-                                           bool have_first) {
-  constexpr int kStep = (LPR / 8) * U;
-  for (int s0 = 0; s0 < S; s0 += kStep) {
-    if (!(have_first && s0 == 0)) issue_chunk<TYPE, LPR, U>(wrow, S, s0, c, wf);
-    // keep every weight load of the chunk ahead of the first dot
-    __builtin_amdgcn_sched_barrier(0);
-    consume_chunk<TYPE, MT, LPR, U>(wf, xq, S, s0, c, acc);
-  }
-}
-
-template <int MT, int LPR, int U>
-__device__ __forceinline__ void stream_row_any(int type, const uint8_t* wrow,
-                                               const qk_q8_block* xq, int S, uint32_t c,
-                                               float (&acc)[MT]) {
-  if (type == QK_TYPE_Q4_K) {
-    Q4KFrag wf[U];
-    stream_row<QK_TYPE_Q4_K, MT, LPR, U>(wrow, xq, S, c, acc, wf, false);
+  // The first U iterations' weights are requested before the activations are
+  // quantised; a quantiser wave's activation loads go out just ahead of them.
+  const int nq = quantiser_waves(MT * (K / 8));
+  const bool quantiser = wave < nq;  // wave-uniform
+  XStage<MT> stage;
+  Piece fa[U], fb[U];
+  Cursor ci{0, 0};
+  if constexpr (!Q8IN)
+    if (quantiser) stage_x<MT>(a.x, M, K, nq, stage);
+  __builtin_amdgcn_sched_barrier(0);
+  issue(ci, fa);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (Q8IN) {
+    copy_q8_into_lds<MT>(a.q8, M, K, xq);
   } else {
-    Q6KFrag wf[U];
-    stream_row<QK_TYPE_Q6_K, MT, LPR, U>(wrow, xq, S, c, acc, wf, false);
+    if (quantiser) quantize_into_lds<MT>(a.x, M, K, nq, stage, xq);
+  }
+  __syncthreads();
+
+  float acc[MT], up[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = up[m] = 0.0f;
+  Cursor cc{0, 0};
+  const int blk_a = piece_block_a(pc, TYPE), blk_step = piece_block_step(TYPE);
+  auto consume = [&](const Piece (&f)[U], int t0) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      if (t0 + i < T) {  // wave-uniform; no global loads inside
+        const int phase = MODE == 1 && cc.k >= ipu;
+        const int kk = phase ? cc.k - ipu : cc.k;
+        const int s_raw = kk * kSPI + sbo;
+        const int blk = min(s_raw, S - 1) * 8 + blk_a;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const qk_q8_block* xr = xq + m * S * 8 + blk;
+          const float v = dot_piece<TYPE>(f[i], load_x(xr), load_x(xr + blk_step), pc, TYPE);
+          const float add = s_raw < S ? v : 0.0f;
+          if (phase) up[m] += add;
+          else acc[m] += add;
+        }
+        if (cc.k == ipu_total - 1) {  // the group's last iteration: reduce and store
+          const int row = group_row(cc.u) + rr;
+          const Where o = locate(min(row, last_row), 0);
+          const bool store = c == 0 && row < row_hi;
+          if constexpr (MODE == 0) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[m] = row_lanes_sum<LPR>(acc[m]);
+            if (store) {
+#pragma unroll
+              for (int m = 0; m < MT; ++m)
+                if (m < M) o.y[static_cast<int64_t>(m) * o.rows + o.local] = acc[m];
+            }
+          } else {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+              acc[m] = row_lanes_sum<LPR>(acc[m]);
+              up[m] = row_lanes_sum<LPR>(up[m]);
+            }
+            if (store) {
+#pragma unroll
+              for (int m = 0; m < MT; ++m) {
+                const float g = acc[m];
+                if (m < M)
+                  a.h[static_cast<int64_t>(m) * o.rows + o.local] = (g / (1.0f + expf(-g))) * up[m];
+              }
+            }
+          }
+#pragma unroll
+          for (int m = 0; m < MT; ++m) acc[m] = up[m] = 0.0f;
+        }
+        advance(cc);
+      }
+    }
+  };
+
+  // Two buffers so the register arrays stay static: the next U iterations
+  // load while the current U are consumed. The last chunk issues nothing
+  // further, and every consume follows its own issue sequence in the code, so
+  // the wait before it counts exactly the loads issued after its buffer.
+  const int nchunks = (T + U - 1) / U;
+  for (int chunk = 0; chunk < nchunks;) {
+    if (chunk + 1 == nchunks) {
+      consume(fa, chunk * U);
+      break;
+    }
+    issue(ci, fb);
+    consume(fa, chunk * U);
+    ++chunk;
+    if (chunk + 1 == nchunks) {
+      consume(fb, chunk * U);
+      break;
+    }
+    issue(ci, fa);
+    consume(fb, chunk * U);
+    ++chunk;
   }
 }
 
 // MODE 0: y_j = x . W_j^T for every segment. MODE 1: segments 0/1 are gate
 // and up of the same shape; h = SiLU(x . gate^T) * (x . up^T).
-// TYPE: the weight type of every segment, or 0 when they differ (then the
-// type is read per unit and the first chunk is not prefetched).
-template <int MT, int LPR, int U, int MODE, int TYPE>
-__global__ __launch_bounds__(256) void matvec_kernel(const MatvecParams p) {
+// TYPE: the weight type of every segment, or 0 for a launch whose segments
+// are Q4_K first, then Q6_K: workgroups below split_wg stream the Q4_K rows
+// [0, split_row), the others the Q6_K rows, each with a body specialised to
+// its type. Q8IN: activations arrive as Q8 blocks (q8) instead of fp32 (x).
+template <int MT, int LPR, int MODE, int TYPE, bool Q8IN>
+__global__ __launch_bounds__(kMatvecThreads) void matvec_kernel(const MatvecParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   qk_q8_block* xq = reinterpret_cast<qk_q8_block*>(lds_raw);
-  constexpr int kRPU = 64 / LPR;  // rows per unit
-  constexpr int kPre = TYPE == 0 ? QK_TYPE_Q4_K : TYPE;
-  const int S = p.S;
-  const uint32_t lane = threadIdx.x & 63u;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int rr = static_cast<int>(lane) / LPR;
-  const uint32_t c = lane % LPR;
-  const int nworkers = static_cast<int>(gridDim.x) * 4;
-  const int first = static_cast<int>(blockIdx.x) * 4 + wave;
+  constexpr int U4 = QK_MATVEC_U4, U6 = QK_MATVEC_U6;
 
-  auto unit_row = [&](int unit, int& j, int& row_raw, int& row) {
-    j = 0;
+  MatvecArgs a;
+  a.x = p.x;
+  a.q8 = p.q8;
+  a.h = p.h;
+  a.M = p.M;
+  a.K = p.K;
+  a.S = p.S;
+  a.nseg = p.nseg;
 #pragma unroll
-    for (int t = 1; t < kMaxSegments; ++t)
-      if (t < p.nseg && unit >= p.seg[t].unit_begin) j = t;
-    row_raw = (unit - p.seg[j].unit_begin) * kRPU + rr;
-    row = min(row_raw, p.seg[j].rows - 1);  // tail lanes re-read the last row
-  };
+  for (int j = 0; j < kMaxSegments; ++j) a.sg[j] = p.seg[j];
+  const int rows_total = p.rows_total, split_wg = p.split_wg, split_row = p.split_row;
+  const int grid = static_cast<int>(gridDim.x);
+  // Every argument (padding included, so no loaded register is recycled for
+  // a later load) is consumed here: the scalar loads are issued together and
+  // waited for once, instead of one round trip per use site.
+  asm volatile("" ::"s"(a.x), "s"(a.q8), "s"(a.h), "s"(a.M), "s"(a.K), "s"(a.S), "s"(a.nseg),
+               "s"(rows_total), "s"(split_wg), "s"(split_row), "s"(p.pad), "s"(grid));
+#pragma unroll
+  for (int j = 0; j < kMaxSegments; ++j)
+    asm volatile("" ::"s"(a.sg[j].w), "s"(a.sg[j].y), "s"(a.sg[j].rows), "s"(a.sg[j].type),
+                 "s"(a.sg[j].row_begin), "s"(a.sg[j].pad));
 
-  // Activation loads first, then the first chunk of this wave's first unit,
-  // so the quantisation below runs while the weight loads are in flight.
-  XStage<MT> stage;
-  if (p.x) stage_x<MT>(p.x, p.M, p.K, stage);
-  __builtin_amdgcn_sched_barrier(0);
-  // Waves without a unit prefetch the last unit (in bounds, unused), so the
-  // loads are issued on every path.
-  typename WeightFrag<kPre>::type pre[U];
-  const bool prefetched = TYPE != 0 && first < p.units;
+  const int wg = static_cast<int>(blockIdx.x);
   if constexpr (TYPE != 0) {
-    int j, row_raw, row;
-    unit_row(min(first, p.units - 1), j, row_raw, row);
-    issue_chunk<TYPE, LPR, U>(p.seg[j].w + static_cast<int64_t>(row) * S * WeightFrag<TYPE>::kBytes,
-                              S, 0, c, pre);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  if (p.x)
-    quantize_into_lds<MT>(p.x, p.M, p.K, stage, xq);
-  else
-    copy_q8_into_lds<MT>(p.q8, p.M, p.K, xq);
-  __syncthreads();
-
-  for (int unit = first; unit < p.units; unit += nworkers) {
-    int j, row_raw, row;
-    unit_row(unit, j, row_raw, row);
-    const int rows = p.seg[j].rows;
-    float acc[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-    if constexpr (TYPE == 0) {
-      const int64_t row_bytes =
-          static_cast<int64_t>(S) * (p.seg[j].type == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes);
-      stream_row_any<MT, LPR, U>(p.seg[j].type, p.seg[j].w + row * row_bytes, xq, S, c, acc);
-    } else {
-      const int64_t row_bytes = static_cast<int64_t>(S) * WeightFrag<TYPE>::kBytes;
-      stream_row<TYPE, MT, LPR, U>(p.seg[j].w + row * row_bytes, xq, S, c, acc, pre,
-                                   prefetched && unit == first);
-    }
-    if constexpr (MODE == 0) {
-#pragma unroll
-      for (int m = 0; m < MT; ++m) acc[m] = row_lanes_sum<LPR>(acc[m]);
-      if (c == 0 && row_raw < rows) {
-#pragma unroll
-        for (int m = 0; m < MT; ++m)
-          if (m < p.M) p.seg[j].y[static_cast<int64_t>(m) * rows + row_raw] = acc[m];
-      }
-    } else {
-      static_assert(MODE == 0 || TYPE != 0, "the FFN mode needs one weight type");
-      float up[MT];
-#pragma unroll
-      for (int m = 0; m < MT; ++m) up[m] = 0.0f;
-      const int64_t row_bytes = static_cast<int64_t>(S) * WeightFrag<kPre>::kBytes;
-      stream_row<kPre, MT, LPR, U>(p.seg[1].w + row * row_bytes, xq, S, c, up, pre, false);
-#pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        acc[m] = row_lanes_sum<LPR>(acc[m]);
-        up[m] = row_lanes_sum<LPR>(up[m]);
-      }
-      if (c == 0 && row_raw < rows) {
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          const float g = acc[m];
-          if (m < p.M) p.h[static_cast<int64_t>(m) * rows + row_raw] = (g / (1.0f + expf(-g))) * up[m];
-        }
-      }
-    }
+    matvec_body<MT, LPR, TYPE == QK_TYPE_Q4_K ? U4 : U6, MODE, TYPE, Q8IN>(a, 0, rows_total, wg,
+                                                                          grid, xq);
+  } else {
+    if (wg < split_wg)
+      matvec_body<MT, LPR, U4, MODE, QK_TYPE_Q4_K, Q8IN>(a, 0, split_row, wg, split_wg, xq);
+    else
+      matvec_body<MT, LPR, U6, MODE, QK_TYPE_Q6_K, Q8IN>(a, split_row, rows_total, wg - split_wg,
+                                                         grid - split_wg, xq);
   }
 }
 
 using MatvecKernel = void (*)(MatvecParams);
 
-// Kernel for MT activation rows, lanes per row `lpr`, unroll `u`, mode and
-// weight type (0 = mixed); nullptr for a combination that is not built.
+// Kernel for MT activation rows, lanes per row `lpr`, mode, weight type
+// (0 = Q4_K and Q6_K segments) and input kind; nullptr for a combination that
+// is not built.
 template <int MT>
-MatvecKernel matvec_kernel_for(int lpr, int u, int mode, int type) {
-  auto by_type = [&](auto lpr_c, auto u_c) -> MatvecKernel {
-    constexpr int L = decltype(lpr_c)::value, UU = decltype(u_c)::value;
-    if (mode == 1) {
-      if (type == QK_TYPE_Q4_K) return &matvec_kernel<MT, L, UU, 1, QK_TYPE_Q4_K>;
-      if (type == QK_TYPE_Q6_K) return &matvec_kernel<MT, L, UU, 1, QK_TYPE_Q6_K>;
+MatvecKernel matvec_kernel_for(int lpr, int mode, int type, bool q8in) {
+  auto pick = [&](auto lpr_c) -> MatvecKernel {
+    constexpr int L = decltype(lpr_c)::value;
+    if (q8in) {
+      if (mode != 0) return nullptr;
+      if (type == QK_TYPE_Q4_K) return &matvec_kernel<MT, L, 0, QK_TYPE_Q4_K, true>;
+      if (type == QK_TYPE_Q6_K) return &matvec_kernel<MT, L, 0, QK_TYPE_Q6_K, true>;
       return nullptr;
     }
-    if (type == QK_TYPE_Q4_K) return &matvec_kernel<MT, L, UU, 0, QK_TYPE_Q4_K>;
-    if (type == QK_TYPE_Q6_K) return &matvec_kernel<MT, L, UU, 0, QK_TYPE_Q6_K>;
-    return &matvec_kernel<MT, L, UU, 0, 0>;
+    if (mode == 1) {
+      if (type == QK_TYPE_Q4_K) return &matvec_kernel<MT, L, 1, QK_TYPE_Q4_K, false>;
+      if (type == QK_TYPE_Q6_K) return &matvec_kernel<MT, L, 1, QK_TYPE_Q6_K, false>;
+      return nullptr;
+    }
+    if (type == QK_TYPE_Q4_K) return &matvec_kernel<MT, L, 0, QK_TYPE_Q4_K, false>;
+    if (type == QK_TYPE_Q6_K) return &matvec_kernel<MT, L, 0, QK_TYPE_Q6_K, false>;
+    return &matvec_kernel<MT, L, 0, 0, false>;
   };
-  using I8 = std::integral_constant<int, 8>;
-  using I16 = std::integral_constant<int, 16>;
-  using I32 = std::integral_constant<int, 32>;
-  using I64 = std::integral_constant<int, 64>;
-  using U2 = std::integral_constant<int, 2>;
-  using U3 = std::integral_constant<int, 3>;
-  using U5 = std::integral_constant<int, 5>;
-  if (lpr == 8) return by_type(I8{}, U5{});
-  if (lpr == 16) return by_type(I16{}, U5{});
-  if (lpr == 32) return by_type(I32{}, U3{});
-  if (u == 2) return by_type(I64{}, U2{});
-  return by_type(I64{}, U5{});
+  switch (lpr) {
+    case 8: return pick(std::integral_constant<int, 8>{});
+    case 16: return pick(std::integral_constant<int, 16>{});
+    case 32: return pick(std::integral_constant<int, 32>{});
+    case 64: return pick(std::integral_constant<int, 64>{});
+    default: return nullptr;
+  }
 }
 
 }  // namespace qk

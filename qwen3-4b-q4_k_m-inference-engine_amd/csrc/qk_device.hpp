@@ -90,26 +90,35 @@ __device__ __forceinline__ float octet_sum(float v) {
   return v;
 }
 
-// Register images of what one lane reads per superblock. Loads and math are
-// split so a wave can issue every load of several superblocks before it
-// consumes the first one.
+// Register images of what one lane reads per superblock piece. A piece is a
+// quarter of a superblock whose bytes are not shared with the other pieces
+// (Q4_K) or share only qh (Q6_K): 64 weights, two Q8 activation blocks.
+// Loads and math are split so a wave can issue every load of several pieces
+// before it consumes the first one.
 struct XFrag {  // one Q8 activation block
   u32x4 c0, c1, rec;
 };
-struct Q4KFrag {  // header + the 32 qs bytes holding sub-blocks 2j, 2j+1
+
+// Q4_K piece j (0..3): the 32 qs bytes 32j..32j+31, whose low nibbles are
+// sub-block 2j and high nibbles sub-block 2j+1, plus the header.
+struct Q4KPiece {
   u32x4 head, q0, q1;
 };
-// Q6_K superblocks sit at 210*s, so odd ones start 2 bytes off a dword.
+
+// Q6_K piece p (0..3) of half h = p/2, parity r = p%2: ql bytes 64h+32r..+31
+// (low nibbles: group r, high nibbles: group r+2 of the half), the half's 32
+// qh bytes (bits 2g..2g+1 of group g), the scale pairs of both groups and d.
+// Q6_K superblocks sit at 210*s, so odd ones start 2 bytes off a dword;
 // 16-byte loads at 2-byte alignment run far slower than dword-aligned ones,
-// so every Q6_K load starts on the dword boundary at or below its field
-// (36 bytes cover 32 field bytes) and v_alignbit realigns in registers.
-struct Q6KFrag {  // 32 ql bytes, 32 qh bytes, the two int8 scales, d
+// so ql/qh loads start on the dword boundary at or below the field (36 bytes
+// cover the 32 field bytes) and v_alignbit realigns in registers.
+struct Q6KPiece {
   u32x4 l0, l1, h0, h1;
   uint32_t l2, h2;   // the dwords after l1 / h1
-  uint32_t sc_word;  // dword holding scales[8h+2g], scales[8h+2g+1]
+  uint32_t sc_a;     // scales[8h+2r], scales[8h+2r+1] (group r)
+  uint32_t sc_b;     // scales[8h+2r+4], scales[8h+2r+5] (group r+2)
   uint32_t d_bits;   // d (2-byte load: a dword could pass the superblock's end)
   uint32_t shift;    // field misalignment in bits: 0 or 16
-  uint32_t sc_shift; // bit offset of the scale pair in sc_word: 0 or 16
 };
 
 __device__ __forceinline__ XFrag load_x(const qk_q8_block* __restrict__ xb) {
@@ -120,72 +129,76 @@ __device__ __forceinline__ XFrag load_x(const qk_q8_block* __restrict__ xb) {
   return f;
 }
 
-__device__ __forceinline__ Q4KFrag load_q4k(const uint8_t* __restrict__ sb, uint32_t g) {
-  Q4KFrag f;
-  f.head = load16(sb);                              // d, dmin, scales[0..11]
-  const uint8_t* qs = sb + 16 + 32 * (g >> 1);
+__device__ __forceinline__ Q4KPiece load_q4k_piece(const uint8_t* __restrict__ sb, uint32_t j) {
+  Q4KPiece f;
+  f.head = load16(sb);  // d, dmin, scales[0..11]
+  const uint8_t* qs = sb + 16 + 32 * j;
   f.q0 = load16(qs);
   f.q1 = load16(qs + 16);
   return f;
 }
 
-// Q6_K lane c covers Q8 block c: h = c/4 selects the 128-weight half, g = c%4
-// the 32-weight group, i.e. the two 16-weight scale groups 8h+2g, 8h+2g+1.
-__device__ __forceinline__ Q6KFrag load_q6k(const uint8_t* __restrict__ sb, uint32_t c) {
-  const uint32_t h = c >> 2;
-  const uint32_t g = c & 3u;
+// Every byte read lies inside the superblock: the ql run ends at most at
+// byte 131 from the dword base, qh at 195, the scale pairs at 207, d at 209.
+__device__ __forceinline__ Q6KPiece load_q6k_piece(const uint8_t* __restrict__ sb, uint32_t p) {
+  const uint32_t h = p >> 1, r = p & 1u;
   const uint32_t mis = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sb)) & 3u;  // 0 or 2
   const uint8_t* base = sb - mis;  // dword-aligned
-  const uint8_t* ql = base + 64 * h + 32 * (g & 1u);
+  const uint8_t* ql = base + 64 * h + 32 * r;
   const uint8_t* qh = base + 128 + 32 * h;
-  Q6KFrag f;
+  Q6KPiece f;
   f.l0 = load16_a4(ql);
   f.l1 = load16_a4(ql + 16);
   f.l2 = load_u32(ql + 32);
   f.h0 = load16_a4(qh);
   f.h1 = load16_a4(qh + 16);
   f.h2 = load_u32(qh + 32);
-  // The scale pair's dword spans at most bytes 204..209 of the superblock.
-  // Shifts are applied in dot_q6k: using a loaded value here would make the
-  // wave wait for the load before it can issue the next superblock's loads.
-  const uint32_t sc_off = 192 + 8 * h + 2 * g + mis;  // from base
-  f.sc_word = load_u32(base + (sc_off & ~3u));
-  f.sc_shift = 8 * (sc_off & 3u);
+  const uint8_t* sc = sb + 192 + 8 * h + 2 * r;  // 2-byte aligned
+  f.sc_a = load_u16(sc);
+  f.sc_b = load_u16(sc + 4);
   f.d_bits = load_u16(sb + 208);
   f.shift = 8 * mis;
   return f;
 }
 
-// Sub-block g (32 weights) of a Q4_K superblock against its Q8 block:
-// xs*(d*sc*dot) - dmin*m*(xs*sum(codes)), the sub-block's term of the
-// reference's per-superblock sum (src/cuda/matmul.cu:24-54).
-__device__ __forceinline__ float dot_q4k(const Q4KFrag& w, const XFrag& x, uint32_t g) {
-  const uint32_t shift = (g & 1u) * 4u;  // low nibble: even g, high: odd g
+// Q4_K piece j against the Q8 blocks of sub-blocks 2j (xa) and 2j+1 (xb):
+// per sub-block xs*(d*sc*dot) - dmin*m*(xs*sum(codes)), the sub-blocks' terms
+// of the reference's per-superblock sum (src/cuda/matmul.cu:24-54).
+__device__ __forceinline__ float dot_q4k_piece(const Q4KPiece& w, const XFrag& xa,
+                                               const XFrag& xb, uint32_t j) {
   constexpr uint32_t kNib = 0x0F0F0F0Fu;
-  int dot = dot4((w.q0.x >> shift) & kNib, x.c0.x, 0);
-  dot = dot4((w.q0.y >> shift) & kNib, x.c0.y, dot);
-  dot = dot4((w.q0.z >> shift) & kNib, x.c0.z, dot);
-  dot = dot4((w.q0.w >> shift) & kNib, x.c0.w, dot);
-  dot = dot4((w.q1.x >> shift) & kNib, x.c1.x, dot);
-  dot = dot4((w.q1.y >> shift) & kNib, x.c1.y, dot);
-  dot = dot4((w.q1.z >> shift) & kNib, x.c1.z, dot);
-  dot = dot4((w.q1.w >> shift) & kNib, x.c1.w, dot);
-  int sc, m;
-  scale_min_k4(g, w.head.y, w.head.z, w.head.w, sc, m);
+  const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+  const uint32_t ca[8] = {xa.c0.x, xa.c0.y, xa.c0.z, xa.c0.w, xa.c1.x, xa.c1.y, xa.c1.z, xa.c1.w};
+  const uint32_t cb[8] = {xb.c0.x, xb.c0.y, xb.c0.z, xb.c0.w, xb.c1.x, xb.c1.y, xb.c1.z, xb.c1.w};
+  int dot_a = 0, dot_b = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    dot_a = dot4(q[i] & kNib, ca[i], dot_a);
+    dot_b = dot4((q[i] >> 4) & kNib, cb[i], dot_b);
+  }
+  int sc_a, m_a, sc_b, m_b;
+  scale_min_k4(2 * j, w.head.y, w.head.z, w.head.w, sc_a, m_a);
+  scale_min_k4(2 * j + 1, w.head.y, w.head.z, w.head.w, sc_b, m_b);
   const float d = half_bits_to_float(w.head.x & 0xFFFFu);
   const float dmin = half_bits_to_float(w.head.x >> 16);
-  const f32x4 rec = __builtin_bit_cast(f32x4, x.rec);
-  // |sc*dot| <= 63*32*15*127 < 2^24, so the integer product converts exactly.
-  const float main_term = d * static_cast<float>(__mul24(sc, dot));
-  return main_term * rec.x - (dmin * static_cast<float>(m)) * rec.y;
+  const f32x4 ra = __builtin_bit_cast(f32x4, xa.rec);
+  const f32x4 rb = __builtin_bit_cast(f32x4, xb.rec);
+  // |sc*dot| <= 63*32*15*127 < 2^24, so the integer products convert exactly.
+  const float main_a = d * static_cast<float>(__mul24(sc_a, dot_a));
+  const float main_b = d * static_cast<float>(__mul24(sc_b, dot_b));
+  return (main_a * ra.x - (dmin * static_cast<float>(m_a)) * ra.y) +
+         (main_b * rb.x - (dmin * static_cast<float>(m_b)) * rb.y);
 }
 
-// Q8 block c of a Q6_K superblock (src/cuda/matmul.cu:61-84):
+// Q6_K piece p against the Q8 blocks of group r (xa) and group r+2 (xb) of
+// its half (src/cuda/matmul.cu:61-84):
 //   q = ((ql >> 4*(g/2)) & 15) | ((qh >> 2g) & 3) << 4, weight = d*sc*(q-32).
-// The -32 offset enters through the Q8 block's neg32 sums as the dots' start.
-__device__ __forceinline__ float dot_q6k(const Q6KFrag& w, const XFrag& x, uint32_t c) {
-  const uint32_t g = c & 3u;
-  const i32x4 rec = __builtin_bit_cast(i32x4, x.rec);
+// The -32 offset enters through the Q8 blocks' neg32 sums as the dots' start.
+__device__ __forceinline__ float dot_q6k_piece(const Q6KPiece& w, const XFrag& xa,
+                                               const XFrag& xb, uint32_t p) {
+  const uint32_t r = p & 1u;
+  const i32x4 ra = __builtin_bit_cast(i32x4, xa.rec);
+  const i32x4 rb = __builtin_bit_cast(i32x4, xb.rec);
   const uint32_t sh = w.shift;
   auto realign = [sh](uint32_t hi, uint32_t lo) { return __builtin_amdgcn_alignbit(hi, lo, sh); };
   const uint32_t l[8] = {realign(w.l0.y, w.l0.x), realign(w.l0.z, w.l0.y), realign(w.l0.w, w.l0.z),
@@ -194,28 +207,32 @@ __device__ __forceinline__ float dot_q6k(const Q6KFrag& w, const XFrag& x, uint3
   const uint32_t q[8] = {realign(w.h0.y, w.h0.x), realign(w.h0.z, w.h0.y), realign(w.h0.w, w.h0.z),
                          realign(w.h1.x, w.h0.w), realign(w.h1.y, w.h1.x), realign(w.h1.z, w.h1.y),
                          realign(w.h1.w, w.h1.z), realign(w.h2, w.h1.w)};
-  const uint32_t lo_shift = 4u * (g >> 1);
-  // rotate so bits (2g, 2g+1) of every byte land on bits 4 and 5
-  const uint32_t hi_rot = (2u * g - 4u) & 31u;
+  const uint32_t ca[8] = {xa.c0.x, xa.c0.y, xa.c0.z, xa.c0.w, xa.c1.x, xa.c1.y, xa.c1.z, xa.c1.w};
+  const uint32_t cb[8] = {xb.c0.x, xb.c0.y, xb.c0.z, xb.c0.w, xb.c1.x, xb.c1.y, xb.c1.z, xb.c1.w};
+  // rotate so bits (2g, 2g+1) of every qh byte land on bits 4 and 5
+  const uint32_t rot_a = (2u * r - 4u) & 31u;  // g = r
+  const uint32_t rot_b = 2u * r;               // g = r + 2: (2(r+2) - 4)
   constexpr uint32_t kLo = 0x0F0F0F0Fu, kHi = 0x30303030u;
-  auto code = [&](uint32_t l, uint32_t h) {
-    return ((l >> lo_shift) & kLo) | (__builtin_amdgcn_alignbit(h, h, hi_rot) & kHi);
-  };
-  int dot_lo = dot4(code(l[0], q[0]), x.c0.x, rec.z);
-  dot_lo = dot4(code(l[1], q[1]), x.c0.y, dot_lo);
-  dot_lo = dot4(code(l[2], q[2]), x.c0.z, dot_lo);
-  dot_lo = dot4(code(l[3], q[3]), x.c0.w, dot_lo);
-  int dot_hi = dot4(code(l[4], q[4]), x.c1.x, rec.w);
-  dot_hi = dot4(code(l[5], q[5]), x.c1.y, dot_hi);
-  dot_hi = dot4(code(l[6], q[6]), x.c1.z, dot_hi);
-  dot_hi = dot4(code(l[7], q[7]), x.c1.w, dot_hi);
-  const uint32_t pair = w.sc_word >> w.sc_shift;
-  const int sc0 = static_cast<int>(static_cast<int8_t>(pair & 0xFFu));
-  const int sc1 = static_cast<int>(static_cast<int8_t>((pair >> 8) & 0xFFu));
-  // |sc*dot| <= 64*16*32*127 per group, the sum < 2^24: exact in fp32.
-  const int isum = __mul24(sc0, dot_lo) + __mul24(sc1, dot_hi);
+  int a_lo = ra.z, a_hi = ra.w, b_lo = rb.z, b_hi = rb.w;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t code_a = (l[i] & kLo) | (__builtin_amdgcn_alignbit(q[i], q[i], rot_a) & kHi);
+    const uint32_t code_b = ((l[i] >> 4) & kLo) | (__builtin_amdgcn_alignbit(q[i], q[i], rot_b) & kHi);
+    if (i < 4) {
+      a_lo = dot4(code_a, ca[i], a_lo);
+      b_lo = dot4(code_b, cb[i], b_lo);
+    } else {
+      a_hi = dot4(code_a, ca[i], a_hi);
+      b_hi = dot4(code_b, cb[i], b_hi);
+    }
+  }
+  auto s8 = [](uint32_t v, int byte) { return static_cast<int>(static_cast<int8_t>((v >> (8 * byte)) & 0xFFu)); };
+  // |sc*dot| <= 64*16*32*127 per group, each sum < 2^24: exact in fp32.
+  const int isum_a = __mul24(s8(w.sc_a, 0), a_lo) + __mul24(s8(w.sc_a, 1), a_hi);
+  const int isum_b = __mul24(s8(w.sc_b, 0), b_lo) + __mul24(s8(w.sc_b, 1), b_hi);
   const float d = half_bits_to_float(w.d_bits);
-  return (d * __builtin_bit_cast(float, rec.x)) * static_cast<float>(isum);
+  return d * (__builtin_bit_cast(float, ra.x) * static_cast<float>(isum_a) +
+              __builtin_bit_cast(float, rb.x) * static_cast<float>(isum_b));
 }
 
 }  // namespace qk

@@ -19,7 +19,7 @@ struct MatvecSegment {
   float* y;
   int32_t rows;
   int32_t type;
-  int32_t unit_begin;  // set by launch_matvec
+  int32_t row_begin;  // first row of this segment in the launch's row space (set by launch_matvec)
   int32_t pad;
 };
 
@@ -29,7 +29,10 @@ struct MatvecParams {
   const float* x;
   const qk_q8_block* q8;
   float* h;  // FFN mode: SiLU(gate)*up output [M x N]
-  int32_t M, K, S, units, nseg, pad;
+  int32_t M, K, S, nseg;
+  int32_t rows_total;           // rows of all segments (FFN mode: of gate)
+  int32_t split_wg, split_row;  // mixed types: workgroups / rows of the Q4_K part
+  int32_t pad;
   MatvecSegment seg[kMaxSegments];
 };
 
