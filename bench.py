@@ -34,6 +34,7 @@ PKG_DIR = ROOT / "qwen3-4b-q4_k_m-inference-engine_amd"
 Q4, Q6 = 12, 14
 SB_BYTES = {Q4: 144, Q6: 210}
 PEAK_HBM_GBS = 8000.0
+PEAK_FP16_TFLOPS = 2500.0  # dense fp16 MFMA
 METRIC = "Q4_K/Q6_K GEMV HBM GB/s (% of peak) at M=1; decode tokens/s, 4B shapes"
 SEED = 20261205  # 20261201 + config id 4
 
@@ -82,21 +83,24 @@ class Op:
 class DecodeSweep:
     """Weights, activations and the per-token launch sequence of the decode sweep."""
 
-    def __init__(self, qk, M: int = 1):
+    def __init__(self, qk, M: int = 1, weights_of: "DecodeSweep | None" = None):
         self.qk, self.M = qk, M
-        self.layers = []
-        tensor = 0
-        for _ in range(N_LAYERS):
-            layer = {}
-            for name, qtype, K, N in LAYER:
-                w = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
-                qk.synth_superblocks(w, qtype, N, K, SEED + 1000 * tensor, 0.01 if qtype == Q4 else 0.005, 0.01)
-                layer[name] = w
-                tensor += 1
-            self.layers.append(layer)
-        name, qtype, K, N = LM_HEAD
-        self.lm_head = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
-        qk.synth_superblocks(self.lm_head, qtype, N, K, SEED + 1000 * tensor, 0.005, 0.01)
+        if weights_of is not None:  # same weights, other activation rows
+            self.layers, self.lm_head = weights_of.layers, weights_of.lm_head
+        else:
+            self.layers = []
+            tensor = 0
+            for _ in range(N_LAYERS):
+                layer = {}
+                for name, qtype, K, N in LAYER:
+                    w = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
+                    qk.synth_superblocks(w, qtype, N, K, SEED + 1000 * tensor, 0.01 if qtype == Q4 else 0.005, 0.01)
+                    layer[name] = w
+                    tensor += 1
+                self.layers.append(layer)
+            name, qtype, K, N = LM_HEAD
+            self.lm_head = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
+            qk.synth_superblocks(self.lm_head, qtype, N, K, SEED + 1000 * tensor, 0.005, 0.01)
         buf = lambda n: qk.DeviceBuffer(4 * M * n)
         self.x_attn, self.x_o, self.x_ffn = buf(2560), buf(4096), buf(2560)
         qk.synth_normal(self.x_attn, M * 2560, SEED + 1)
@@ -201,6 +205,82 @@ def measured_traffic(family: str):
         return None
 
 
+COPIES = 40  # distinct weight copies per single-GEMV config: > 2x the 256 MB MALL
+
+
+def time_launches(qk, stream, calls, replays: int = 5) -> float:
+    """Average microseconds per launch of `calls`, captured back to back in a
+    graph and replayed between HIP events on the launch stream."""
+    graph = qk.Graph.capture(stream, lambda: [c() for c in calls])
+    ms = time_graph(qk, graph, stream, 2, replays)
+    graph.destroy()
+    return 1000.0 * ms / len(calls)
+
+
+def single_gemv(qk, stream, qtype: int, K: int, N: int, config_id: int):
+    """Configs 0/1: one M=1 mat-vec over COPIES distinct weight copies."""
+    seed = 20261201 + config_id
+    ws = []
+    for c in range(COPIES):
+        w = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
+        qk.synth_superblocks(w, qtype, N, K, seed + 7919 * c, 0.01 if qtype == Q4 else 0.005, 0.01)
+        ws.append(w)
+    x, y = qk.DeviceBuffer(4 * K), qk.DeviceBuffer(4 * N)
+    qk.synth_normal(x, K, seed)
+    qk.synchronize()
+    us = time_launches(qk, stream, [lambda w=w: qk.matmul(x, w, qtype, K, N, y, 1, stream) for w in ws])
+    nbytes = gemv_bytes(qtype, K, N, 1)
+    for w in ws:
+        w.free()
+    return {"shape": f"{'Q4_K' if qtype == Q4 else 'Q6_K'} {N}x{K}, M=1, {COPIES} weight copies",
+            "avg_us": round(us, 3), "GB/s": round(nbytes / (us * 1e3), 1),
+            "frac": round(nbytes / (us * 1e3) / PEAK_HBM_GBS, 4), "GFLOP/s": round(2 * N * K / (us * 1e3), 1)}
+
+
+def prefill_gemm(qk, stream):
+    """Config 3: M=512 prefill projections (gate, q, k, v) on the MFMA GEMM."""
+    M, K = 512, 2560
+    out = {}
+    x = qk.DeviceBuffer(4 * M * K)
+    qk.synth_normal(x, M * K, 20261204)
+    for name, qtype, N in (("ffn_gate", Q4, 9728), ("attn_q", Q4, 4096), ("attn_k", Q4, 1024), ("attn_v", Q6, 1024)):
+        w = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
+        qk.synth_superblocks(w, qtype, N, K, 20261204 + N, 0.01 if qtype == Q4 else 0.005, 0.01)
+        y = qk.DeviceBuffer(4 * M * N)
+        need = qk.matmul_workspace_size(qtype, K, N, M)
+        ws = qk.DeviceBuffer(need)
+        qk.synchronize()
+        us = time_launches(qk, stream, [lambda w=w, y=y, ws=ws: qk.matmul_ws(x, w, qtype, K, N, y, M, ws, need, stream)] * 10)
+        flops = 2 * M * N * K
+        out[name] = {"shape": f"M={M} K={K} N={N} {'Q4_K' if qtype == Q4 else 'Q6_K'}",
+                     "avg_us": round(us, 2), "TFLOP/s": round(flops / (us * 1e6), 1),
+                     "frac_of_fp16_mfma_peak": round(flops / (us * 1e6) / PEAK_FP16_TFLOPS, 4)}
+        for b in (w, y, ws):
+            b.free()
+    x.free()
+    return out
+
+
+def measure_configs(qk, sweep: DecodeSweep, stream):
+    """The other BASELINE configurations, reported beside the headline sweep."""
+    out = {"0_q4k_gemv": single_gemv(qk, stream, Q4, 2560, 9728, 0),
+           "1_q6k_gemv": single_gemv(qk, stream, Q6, 9728, 2560, 1)}
+    ffn = [op for op in sweep.ops(stream) if op.family in ("ffn_gate_up", "ffn_down")]
+    us = time_launches(qk, stream, [op.call for op in ffn]) * len(ffn)
+    nbytes = sum(op.nbytes for op in ffn)
+    out["2_ffn_block_sweep"] = {"shape": "36 x (gate+up SiLU, down), M=1", "us_per_sweep": round(us, 1),
+                                "GB/s": round(nbytes / (us * 1e3), 1),
+                                "frac": round(nbytes / (us * 1e3) / PEAK_HBM_GBS, 4)}
+    out["3_prefill_gemm"] = prefill_gemm(qk, stream)
+    sweep8 = DecodeSweep(qk, M=8, weights_of=sweep)
+    graph = qk.Graph.capture(stream, lambda: sweep8.record(stream))
+    ms = time_graph(qk, graph, stream, 2, 10)
+    graph.destroy()
+    out["4_decode_sweep_m8"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(8e3 / ms, 1),
+                                "GB/s": round(sweep8.bytes_per_step() / (ms * 1e6), 1)}
+    return out
+
+
 def cpu_baseline(qk, sweep: DecodeSweep, budget_s: float):
     """The CPU oracle (OpenMP, double accumulation) on a bounded sample: the
     projections of layer 0, repeated until ~budget_s of CPU work."""
@@ -251,6 +331,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configurations")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -291,6 +372,11 @@ def main() -> int:
                     "avg_launch_us": d["avg_us"], "avg_bytes_per_launch": d["avg_bytes"]}
         log(f"kernels: {json.dumps(kernels)}")
 
+    configs = None
+    if not args.no_configs:
+        configs = measure_configs(qk, sweep, stream)
+        log(f"configs: {json.dumps(configs)}")
+
     baseline = None
     if args.cpu_seconds > 0:
         log("CPU baseline (oracle, OpenMP) ...")
@@ -312,6 +398,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": baseline,
         "kernels": kernels,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -49,7 +49,7 @@ hipError_t device_facts(DeviceFacts& out) {
   return hipSuccess;
 }
 
-hipError_t blocks_per_cu(MatvecKernel fn, size_t lds, int& out) {
+hipError_t blocks_per_cu(MatvecKernel fn, int threads, size_t lds, int& out) {
   std::lock_guard<std::mutex> lock(g_mutex);
   const auto key = std::make_pair(fn, lds);
   auto it = g_occupancy.find(key);
@@ -59,7 +59,7 @@ hipError_t blocks_per_cu(MatvecKernel fn, size_t lds, int& out) {
                                        static_cast<int>(lds));
     if (e != hipSuccess) return e;
     int n = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kMatvecThreads, lds);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds);
     if (e != hipSuccess) return e;
     it = g_occupancy.emplace(key, std::max(n, 1)).first;
   }
@@ -103,6 +103,7 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
   if (e != hipSuccess) return e;
   const int M = p.M;
   const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const int waves = mt == 1 ? matvec_waves<1>() : matvec_waves<8>();
   const size_t lds = static_cast<size_t>(mt) * static_cast<size_t>(p.K / 32) * sizeof(qk_q8_block);
   if (lds > dev.max_lds) return hipErrorInvalidValue;
 
@@ -128,7 +129,7 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
   const MatvecKernel probe = pick_kernel(mt, 8, mode, type, p.x == nullptr);
   if (!probe) return hipErrorInvalidValue;
   int per_cu = 1;
-  e = blocks_per_cu(probe, lds, per_cu);
+  e = blocks_per_cu(probe, 64 * waves, lds, per_cu);
   if (e != hipSuccess) return e;
   const int64_t grid = std::min<int64_t>(static_cast<int64_t>(dev.cus) * per_cu, begin);
   int64_t wg4 = grid;
@@ -149,9 +150,9 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
     if (cand != QK_MATVEC_FORCE_LPR) continue;
 #endif
     int64_t cost = 0;
-    if (rows4) cost = std::max(cost, wave_iterations(rows4, wg4 * kMatvecWaves, cand, p.S, mode) * kQ4KBytes);
+    if (rows4) cost = std::max(cost, wave_iterations(rows4, wg4 * waves, cand, p.S, mode) * kQ4KBytes);
     if (rows6)
-      cost = std::max(cost, wave_iterations(rows6, (type == 0 ? grid - wg4 : grid) * kMatvecWaves, cand,
+      cost = std::max(cost, wave_iterations(rows6, (type == 0 ? grid - wg4 : grid) * waves, cand,
                                             p.S, mode) * kQ6KBytes);
     if (cost < best) {
       best = cost;
@@ -160,9 +161,9 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
   }
   const MatvecKernel fn = pick_kernel(mt, lpr, mode, type, p.x == nullptr);
   if (!fn) return hipErrorInvalidValue;
-  e = blocks_per_cu(fn, lds, per_cu);  // sets the kernel's dynamic LDS limit
+  e = blocks_per_cu(fn, 64 * waves, lds, per_cu);  // sets the kernel's dynamic LDS limit
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(grid)), dim3(kMatvecThreads), lds, stream, p);
+  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(grid)), dim3(64 * waves), lds, stream, p);
   return hipGetLastError();
 }
 

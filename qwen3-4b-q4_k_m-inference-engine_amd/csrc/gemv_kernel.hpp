@@ -37,6 +37,9 @@ namespace qk {
 #ifndef QK_MATVEC_WAVES
 #define QK_MATVEC_WAVES 16
 #endif
+#ifndef QK_MATVEC_WAVES_MT
+#define QK_MATVEC_WAVES_MT 8  // M > 1: several accumulators per lane need 256 VGPRs
+#endif
 #ifndef QK_MATVEC_U4
 #define QK_MATVEC_U4 2
 #endif
@@ -46,8 +49,11 @@ namespace qk {
 #ifndef QK_MATVEC_XSTAGED
 #define QK_MATVEC_XSTAGED 2
 #endif
-constexpr int kMatvecWaves = QK_MATVEC_WAVES;
-constexpr int kMatvecThreads = 64 * kMatvecWaves;
+// Waves per workgroup for MT activation rows.
+template <int MT>
+constexpr int matvec_waves() {
+  return MT == 1 ? QK_MATVEC_WAVES : QK_MATVEC_WAVES_MT;
+}
 
 // Per-lane register image of one iteration's piece.
 template <int TYPE>
@@ -147,8 +153,9 @@ struct XStage {
 };
 
 // Quantiser waves for `tasks` tasks: enough for kXStaged tasks per lane.
+template <int MT>
 __device__ __forceinline__ int quantiser_waves(int tasks) {
-  return min(kMatvecWaves, (tasks + 64 * kXStaged - 1) / (64 * kXStaged));
+  return min(matvec_waves<MT>(), (tasks + 64 * kXStaged - 1) / (64 * kXStaged));
 }
 
 // Loads of every staged task are unconditional (indices clamped into the
@@ -212,7 +219,7 @@ __device__ void copy_q8_into_lds(const qk_q8_block* __restrict__ q8, int M, int 
   const int per_row = (K / 32) * 3;  // 16-byte chunks
   const u32x4* src = reinterpret_cast<const u32x4*>(q8);
   u32x4* dst = reinterpret_cast<u32x4*>(lds);
-  for (int t = threadIdx.x; t < MT * per_row; t += kMatvecThreads) {
+  for (int t = threadIdx.x; t < MT * per_row; t += 64 * matvec_waves<MT>()) {
     const int m = t / per_row;
     dst[t] = m < M ? src[t] : u32x4{0u, 0u, 0u, 0u};
   }
@@ -272,7 +279,7 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs& a, int row_lo, int
   // g % nworkers, worker = wave*nwg + wg, so consecutive groups run on
   // different CUs and, at any moment, the whole GPU streams one compact
   // window of the matrix (DRAM rows stay open for many requests).
-  const int nworkers = nwg * kMatvecWaves;
+  const int nworkers = nwg * matvec_waves<MT>();
   const int wid = wave * nwg + wg;
   const int groups_total = (row_hi - row_lo + kRPU - 1) / kRPU;
   const int ngroups = wid < groups_total ? (groups_total - 1 - wid) / nworkers + 1 : 0;
@@ -329,7 +336,7 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs& a, int row_lo, int
 
   // The first U iterations' weights are requested before the activations are
   // quantised; a quantiser wave's activation loads go out just ahead of them.
-  const int nq = quantiser_waves(MT * (K / 8));
+  const int nq = quantiser_waves<MT>(MT * (K / 8));
   const bool quantiser = wave < nq;  // wave-uniform
   XStage<MT> stage;
   Piece fa[U], fb[U];
@@ -432,7 +439,7 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs& a, int row_lo, int
 // [0, split_row), the others the Q6_K rows, each with a body specialised to
 // its type. Q8IN: activations arrive as Q8 blocks (q8) instead of fp32 (x).
 template <int MT, int LPR, int MODE, int TYPE, bool Q8IN>
-__global__ __launch_bounds__(kMatvecThreads) void matvec_kernel(const MatvecParams p) {
+__global__ __launch_bounds__(64 * matvec_waves<MT>()) void matvec_kernel(const MatvecParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   qk_q8_block* xq = reinterpret_cast<qk_q8_block*>(lds_raw);
   constexpr int U4 = QK_MATVEC_U4, U6 = QK_MATVEC_U6;

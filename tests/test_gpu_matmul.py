@@ -320,14 +320,15 @@ def test_ffn_gate_up_silu(gpu, oracle, qtype, M):
     err = oracle.row_norm_error(got, ref)
     print(f"ffn row-norm error {err:.3e}")
     assert err <= 1e-5
-    # the same numbers as two mat-vecs and the separate SiLU kernel
+    # the same numbers as two mat-vecs and the separate SiLU kernel, up to the
+    # order of the fp32 sums (the launches may split rows over lanes differently)
     gd, ud = gpu.DeviceBuffer(4 * M * N), gpu.DeviceBuffer(4 * M * N)
     gpu.matmul(xd, gate, qtype, K, N, gd, M)
     gpu.matmul(xd, up, qtype, K, N, ud, M)
     sep = gpu.DeviceBuffer(4 * M * N)
     gpu.silu_multiply(gd, ud, sep, M * N)
     gpu.synchronize()
-    assert np.allclose(got, sep.download(np.float32).reshape(M, N), rtol=1e-6, atol=1e-6)
+    assert oracle.row_norm_error(got, sep.download(np.float32).reshape(M, N).astype(np.float64)) <= 1e-6
 
 
 def test_prologue_quantisation_matches_quantize_kernel(gpu, oracle):
