@@ -4,11 +4,12 @@
 Workload (one "step" = one decoded token's projection sweep): a random-init
 Qwen3-4B Q4_K_M layout, 36 layers x {attn_q, attn_k (Q4_K 2560->4096/1024),
 attn_v (Q6_K 2560->1024), attn_output (Q4_K 4096->2560), ffn_gate, ffn_up
-(Q4_K 2560->9728), ffn_down (Q6_K 9728->2560)} + lm_head (Q6_K 2560->151936),
-M = 1 activation row, in the reference engine's call order
-(src/Engine.cpp:83-109): Q8 quantize + mat-vec per projection, SiLU*up before
-ffn_down. Weights (2.62 GB) are generated on the device; activations are
-N(0,1). The step is captured once as a graph and replayed.
+(Q4_K 2560->9728), ffn_down (Q6_K 9728->2560)} + lm_head (Q6_K 2560->151936)
+with the next-token argmax, M = 1 activation row, in the reference engine's
+call order (src/Engine.cpp:83-111): Q8 quantize + mat-vec per projection,
+SiLU*up before ffn_down, lm_head + argmax in one launch. Weights (2.62 GB)
+are generated on the device; activations are N(0,1). The step is captured
+once as a graph and replayed.
 
 Prints one JSON line: value = algorithmic GB/s of the whole sweep
 (weights + fp32 activations in/out, see gemv_bytes), plus tokens/s, the
@@ -109,6 +110,10 @@ class DecodeSweep:
         self.y = {n: buf(N) for n, _, _, N in LAYER}
         self.h = buf(9728)
         self.logits = buf(LM_HEAD[3])
+        self.argmax_bytes = qk.argmax_workspace_size()
+        self.argmax_ws = qk.DeviceBuffer(self.argmax_bytes)
+        qk.check(qk.load().qk_memset_async(self.argmax_ws.ptr, 0, self.argmax_bytes, None))
+        self.next_token = qk.DeviceBuffer(4)
         qk.synchronize()
 
     def ops(self, stream):
@@ -132,8 +137,13 @@ class DecodeSweep:
             out.append(Op("ffn_down", gemv_bytes(Q6, 9728, 2560, M),
                           lambda w=w_d: qk.matmul(self.h, w, Q6, 9728, 2560, y["ffn_down"], M, stream)))
         name, qtype, K, N = LM_HEAD
-        out.append(Op("lm_head", gemv_bytes(qtype, K, N, M),
-                      lambda: qk.matmul(self.x_attn, self.lm_head, qtype, K, N, self.logits, M, stream)))
+        if M == 1:  # the engine's last step: logits of the final position and their argmax
+            out.append(Op("lm_head_argmax", weight_bytes(qtype, K, N) + 4 * K + 4,
+                          lambda: qk.matmul_argmax(self.x_attn, self.lm_head, qtype, K, N, None,
+                                                   self.next_token, self.argmax_ws, self.argmax_bytes, stream)))
+        else:
+            out.append(Op("lm_head", gemv_bytes(qtype, K, N, M),
+                          lambda: qk.matmul(self.x_attn, self.lm_head, qtype, K, N, self.logits, M, stream)))
         return out
 
     def bytes_per_step(self) -> int:
@@ -391,7 +401,8 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic",
         "config": {"workload": "Qwen3-4B Q4_K_M decode projection sweep, M=1: 36 x (q,k,v,o,gate,up,down) "
-                               "+ lm_head 151936x2560 Q6_K, Q8 activations, 4 launches/layer, graph-replayed",
+                               "+ lm_head 151936x2560 Q6_K with next-token argmax, Q8 activations, "
+                               "4 launches/layer + 1, graph-replayed",
                    "tokens_per_s": round(1e3 / ms, 2), "bytes_per_step": bytes_step,
                    "frac_of_peak_hbm": round(gbs / PEAK_HBM_GBS, 4), "eager_ms_per_step": round(eager_ms, 3),
                    "device": info["name"], "arch": info["arch"]},

@@ -64,6 +64,12 @@ void matmul(const float* input, const Weight& weight, float* output, size_t rows
 // out = gate/(1+exp(-gate)) * up (src/cuda/silu_multiply.cu:19-23).
 void silu_multiply(const float* gate, const float* up, float* output, size_t count);
 
+// Index of the largest logit: lowest index among equal maxima, NaN and -inf
+// never win, 0xFFFFFFFF when nothing wins; blocks until the index is on the
+// host (src/cuda/argmax.cu:71-98). Throws std::invalid_argument for a null
+// pointer or a size outside [1, 2^32-1].
+uint32_t argmax(const float* logits, size_t vocabulary_size);
+
 // Superblock rows -> fp32 (src/cuda/embedding.cu:65-84).
 void dequantize_embeddings(const void* packed, float* output, size_t rows,
     size_t width, size_t row_bytes, ggml_type type);

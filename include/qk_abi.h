@@ -118,6 +118,29 @@ int qk_matmul_segments(const float *x, int64_t M, int64_t K, const qk_segment *s
 int qk_ffn_gate_up(const float *x, const void *gate, const void *up, int type, int64_t K,
                    int64_t N, float *h, int64_t M, qk_stream_t stream);
 
+/* Bytes of the workspace qk_argmax / qk_matmul_argmax need. The caller
+ * zero-fills it once before its first use (qk_memset_async or hipMemset);
+ * every call leaves it ready for the next. Calls that may run concurrently
+ * (different streams) need separate workspaces. */
+size_t qk_argmax_workspace_size(void);
+
+/* *result (device uint32) = the index of the largest of logits[0, count): the
+ * lowest index among equal maxima; NaN and -inf never win; 0xFFFFFFFF if no
+ * entry wins. Replaces kernels::argmax (include/Kernels.hpp:77,
+ * src/cuda/argmax.cu:71-98) without its blocking copy: the result stays on the
+ * device. count in [1, 2^32-1], else QK_ERR_INVALID_ARGUMENT. */
+int qk_argmax(const float *logits, int64_t count, uint32_t *result, void *workspace,
+              size_t workspace_bytes, qk_stream_t stream);
+
+/* lm_head and argmax in one launch for one activation row: logits[N] =
+ * Q8(x)[K] . W^T (written only if logits != NULL) and *result = the argmax of
+ * the logits, with qk_argmax's rules. Replaces kernels::matmul + kernels::argmax
+ * at src/Engine.cpp:106-111. Validation as qk_matmul with M = 1, plus
+ * qk_argmax's result and workspace rules. */
+int qk_matmul_argmax(const float *x, const void *w, int type, int64_t K, int64_t N, float *logits,
+                     uint32_t *result, void *workspace, size_t workspace_bytes,
+                     qk_stream_t stream);
+
 /* Dequantize `rows` rows of K weights (row stride row_bytes) to fp32
  * out[rows x K], bit-identical to the formulas of src/cuda/embedding.cu:6-59.
  * Replaces kernels::dequantize_embeddings (include/Kernels.hpp:74-75,

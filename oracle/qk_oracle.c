@@ -384,14 +384,21 @@ void qko_silu_multiply(const float *gate, const float *up, float *out, int64_t c
     }
 }
 
-/* src/cuda/argmax.cu:25-98: largest score, lowest index on ties. */
+/* src/cuda/argmax.cu:25-98: the candidate starts at (SIZE_MAX, -inf) (:13-15)
+ * and is replaced only by a strictly greater score (:32), ties across threads
+ * going to the lower index (:19-23): the first index of the largest value;
+ * NaN and -inf never win; if nothing wins, SIZE_MAX, which the uint32_t
+ * return (:96) makes 0xFFFFFFFF. */
 int64_t qko_argmax(const float *v, int64_t count)
 {
-    int64_t best = 0;
-    for (int64_t i = 1; i < count; ++i)
-        if (v[i] > v[best])
+    int64_t best = -1;
+    float score = -INFINITY;
+    for (int64_t i = 0; i < count; ++i)
+        if (v[i] > score) {
+            score = v[i];
             best = i;
-    return count > 0 ? best : -1;
+        }
+    return best < 0 ? (int64_t)0xFFFFFFFFu : best;
 }
 
 /* ------------------------------------------------------------ synthetic --- */

@@ -65,6 +65,10 @@ _SIGNATURES = {
     "qk_matmul_segments": [_c_void_p, _i64, _i64, ctypes.POINTER(Segment), _int, _c_void_p],
     "qk_ffn_gate_up": [_c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _i64,
                        _c_void_p],
+    "qk_argmax_workspace_size": [],
+    "qk_argmax": [_c_void_p, _i64, _c_void_p, _c_void_p, _size, _c_void_p],
+    "qk_matmul_argmax": [_c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+                         _size, _c_void_p],
     "qk_dequantize_rows": [_c_void_p, _c_void_p, _i64, _i64, _size, _int, _c_void_p],
     "qk_silu_multiply": [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
     "qk_malloc": [ctypes.POINTER(_c_void_p), _size],
@@ -95,7 +99,8 @@ _SIGNATURES = {
     "qk_synth_superblocks": [_c_void_p, _int, _i64, _i64, _u64, _float, _float, _c_void_p],
     "qk_synth_normal": [_c_void_p, _i64, _u64, _c_void_p],
 }
-_RESTYPES = {"qk_last_error": ctypes.c_char_p, "qk_matmul_workspace_size": _size}
+_RESTYPES = {"qk_last_error": ctypes.c_char_p, "qk_matmul_workspace_size": _size,
+             "qk_argmax_workspace_size": _size}
 
 _LIB = None
 _SHUTTING_DOWN = False
@@ -338,6 +343,23 @@ def matmul_ws(x, w, qtype: int, K: int, N: int, y, M: int, workspace, workspace_
               stream=None) -> None:
     check(load().qk_matmul_ws(_ptr(x), _ptr(w), qtype, K, N, _ptr(y), M, _ptr(workspace),
                               workspace_bytes, _stream_ptr(stream)))
+
+
+def argmax_workspace_size() -> int:
+    return int(load().qk_argmax_workspace_size())
+
+
+def argmax(logits, count: int, result, workspace, workspace_bytes: int, stream=None) -> None:
+    """*result (device uint32) = argmax of logits[0, count) (qk_argmax)."""
+    check(load().qk_argmax(_ptr(logits), count, _ptr(result), _ptr(workspace), workspace_bytes,
+                           _stream_ptr(stream)))
+
+
+def matmul_argmax(x, w, qtype: int, K: int, N: int, logits, result, workspace,
+                  workspace_bytes: int, stream=None) -> None:
+    """lm_head + argmax in one launch (qk_matmul_argmax); logits may be None."""
+    check(load().qk_matmul_argmax(_ptr(x), _ptr(w), qtype, K, N, _ptr(logits), _ptr(result),
+                                  _ptr(workspace), workspace_bytes, _stream_ptr(stream)))
 
 
 def quantize_q8(x, M: int, K: int, q8, stream=None) -> None:

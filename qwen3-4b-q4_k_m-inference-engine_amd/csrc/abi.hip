@@ -9,6 +9,7 @@
 #include <cstring>
 #include <algorithm>
 #include <string>
+#include <cstdint>
 
 #include "qk_abi.h"
 #include "qk_launch.hpp"
@@ -85,6 +86,15 @@ int run_matvec(qk::MatvecParams base, int64_t M, int64_t K, int mode, hipStream_
     const hipError_t error = qk::launch_matvec(p, mode, stream);
     if (error != hipSuccess) return hip_fail(error, "matmul launch failed");
   }
+  return QK_OK;
+}
+
+int validate_argmax_output(const uint32_t* result, const void* workspace, size_t workspace_bytes) {
+  if (!result) return fail(QK_ERR_INVALID_ARGUMENT, "argmax result pointer must be non-null");
+  if (!workspace || workspace_bytes < qk::argmax_workspace_bytes() ||
+      reinterpret_cast<uintptr_t>(workspace) % 8 != 0)
+    return fail(QK_ERR_INVALID_ARGUMENT,
+                "argmax workspace must be 8-byte aligned and hold qk_argmax_workspace_size() bytes");
   return QK_OK;
 }
 
@@ -244,6 +254,36 @@ int qk_ffn_gate_up(const float* x, const void* gate, const void* up, int type, i
   p.seg[0] = {static_cast<const uint8_t*>(gate), nullptr, static_cast<int32_t>(N), type, 0, 0};
   p.seg[1] = {static_cast<const uint8_t*>(up), nullptr, static_cast<int32_t>(N), type, 0, 0};
   return run_matvec(p, M, K, 1, as_stream(stream));
+}
+
+size_t qk_argmax_workspace_size(void) { return qk::argmax_workspace_bytes(); }
+
+int qk_argmax(const float* logits, int64_t count, uint32_t* result, void* workspace,
+              size_t workspace_bytes, qk_stream_t stream) {
+  // src/cuda/argmax.cu:73-74
+  if (!logits || count <= 0 || count > int64_t{UINT32_MAX})
+    return fail(QK_ERR_INVALID_ARGUMENT, "Invalid argmax input");
+  const int status = validate_argmax_output(result, workspace, workspace_bytes);
+  if (status != QK_OK) return status;
+  const hipError_t error = qk::launch_argmax(logits, count, workspace, result, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "argmax launch failed");
+}
+
+int qk_matmul_argmax(const float* x, const void* w, int type, int64_t K, int64_t N, float* logits,
+                     uint32_t* result, void* workspace, size_t workspace_bytes, qk_stream_t stream) {
+  int status = validate_matmul(type, K, N, 1);
+  if (status != QK_OK) return status;
+  if (!x || !w) return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
+  status = validate_argmax_output(result, workspace, workspace_bytes);
+  if (status != QK_OK) return status;
+  status = validate_weight_pointer(w, type);
+  if (status != QK_OK) return status;
+  qk::MatvecParams p = params_for(x, nullptr);
+  p.nseg = 1;
+  p.seg[0] = {static_cast<const uint8_t*>(w), logits, static_cast<int32_t>(N), type, 0, 0};
+  p.argmax_ws = workspace;
+  p.argmax_result = result;
+  return run_matvec(p, 1, K, 2, as_stream(stream));
 }
 
 int qk_dequantize_rows(const void* packed, float* out, int64_t rows, int64_t K, size_t row_bytes,

@@ -131,7 +131,8 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
   int per_cu = 1;
   e = blocks_per_cu(probe, 64 * waves, lds, per_cu);
   if (e != hipSuccess) return e;
-  const int64_t grid = std::min<int64_t>(static_cast<int64_t>(dev.cus) * per_cu, begin);
+  int64_t grid = std::min<int64_t>(static_cast<int64_t>(dev.cus) * per_cu, begin);
+  if (mode == 2) grid = std::min<int64_t>(grid, kArgmaxSlots);  // one partial per workgroup
   int64_t wg4 = grid;
   if (type == 0) {
     if (grid < 2) return hipErrorInvalidValue;  // rows_total >= 2 here

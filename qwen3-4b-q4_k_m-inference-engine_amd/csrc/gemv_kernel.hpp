@@ -24,6 +24,7 @@
 
 #include <type_traits>
 
+#include "argmax.hpp"
 #include "qk_device.hpp"
 #include "qk_launch.hpp"
 
@@ -257,12 +258,14 @@ struct MatvecArgs {
   MatvecSegment sg[kMaxSegments];
 };
 
+
 // One weight type's share of a launch: rows [row_lo, row_hi) of the
 // concatenated segments, streamed by workgroups wg of nwg, in groups of kRPU
 // rows with each row's LPR lanes covering LPR/4 superblocks per iteration.
+// Returns the thread's best argmax key (argmax mode; 0 otherwise).
 template <int MT, int LPR, int U, int MODE, int TYPE, bool Q8IN>
-__device__ __forceinline__ void matvec_body(const MatvecArgs& a, int row_lo, int row_hi, int wg,
-                                            int nwg, qk_q8_block* __restrict__ xq) {
+__device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo, int row_hi, int wg,
+                                                int nwg, qk_q8_block* __restrict__ xq) {
   using Piece = typename PieceOf<TYPE>::type;
   constexpr int kRPU = 64 / LPR;  // rows per group
   constexpr int kSPI = LPR / 4;   // superblocks per iteration
@@ -356,6 +359,7 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs& a, int row_lo, int
   float acc[MT], up[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m) acc[m] = up[m] = 0.0f;
+  uint64_t best_key = 0;  // argmax mode
   Cursor cc{0, 0};
   const int blk_a = piece_block_a(pc, TYPE), blk_step = piece_block_step(TYPE);
   auto consume = [&](const Piece (&f)[U], int t0) {
@@ -385,6 +389,12 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs& a, int row_lo, int
 #pragma unroll
               for (int m = 0; m < MT; ++m)
                 if (m < M) o.y[static_cast<int64_t>(m) * o.rows + o.local] = acc[m];
+            }
+          } else if constexpr (MODE == 2) {
+            acc[0] = row_lanes_sum<LPR>(acc[0]);
+            if (store) {
+              if (o.y) o.y[o.local] = acc[0];
+              best_key = max_key(best_key, argmax_key(acc[0], static_cast<uint32_t>(o.local)));
             }
           } else {
 #pragma unroll
@@ -430,10 +440,13 @@ __device__ __forceinline__ void matvec_body(const MatvecArgs& a, int row_lo, int
     consume(fb, chunk * U);
     ++chunk;
   }
+  return best_key;
 }
 
 // MODE 0: y_j = x . W_j^T for every segment. MODE 1: segments 0/1 are gate
-// and up of the same shape; h = SiLU(x . gate^T) * (x . up^T).
+// and up of the same shape; h = SiLU(x . gate^T) * (x . up^T). MODE 2 (M = 1,
+// one segment, lm_head): y (optional) and the index of its largest entry,
+// reduced across the launch (src/Engine.cpp:106-111, src/cuda/argmax.cu).
 // TYPE: the weight type of every segment, or 0 for a launch whose segments
 // are Q4_K first, then Q6_K: workgroups below split_wg stream the Q4_K rows
 // [0, split_row), the others the Q6_K rows, each with a body specialised to
@@ -459,8 +472,11 @@ __global__ __launch_bounds__(64 * matvec_waves<MT>()) void matvec_kernel(const M
   // Every argument (padding included, so no loaded register is recycled for
   // a later load) is consumed here: the scalar loads are issued together and
   // waited for once, instead of one round trip per use site.
+  void* const argmax_ws = p.argmax_ws;
+  uint32_t* const argmax_result = p.argmax_result;
   asm volatile("" ::"s"(a.x), "s"(a.q8), "s"(a.h), "s"(a.M), "s"(a.K), "s"(a.S), "s"(a.nseg),
-               "s"(rows_total), "s"(split_wg), "s"(split_row), "s"(p.pad), "s"(grid));
+               "s"(rows_total), "s"(split_wg), "s"(split_row), "s"(p.pad), "s"(grid),
+               "s"(argmax_ws), "s"(argmax_result));
 #pragma unroll
   for (int j = 0; j < kMaxSegments; ++j)
     asm volatile("" ::"s"(a.sg[j].w), "s"(a.sg[j].y), "s"(a.sg[j].rows), "s"(a.sg[j].type),
@@ -468,8 +484,13 @@ __global__ __launch_bounds__(64 * matvec_waves<MT>()) void matvec_kernel(const M
 
   const int wg = static_cast<int>(blockIdx.x);
   if constexpr (TYPE != 0) {
-    matvec_body<MT, LPR, TYPE == QK_TYPE_Q4_K ? U4 : U6, MODE, TYPE, Q8IN>(a, 0, rows_total, wg,
-                                                                          grid, xq);
+    const uint64_t key = matvec_body<MT, LPR, TYPE == QK_TYPE_Q4_K ? U4 : U6, MODE, TYPE, Q8IN>(
+        a, 0, rows_total, wg, grid, xq);
+    if constexpr (MODE == 2) {
+      __shared__ uint64_t keys[matvec_waves<MT>() + 1];
+      argmax_finish(key, static_cast<ArgmaxWorkspace*>(argmax_ws), argmax_result, keys,
+                    matvec_waves<MT>());
+    }
   } else {
     if (wg < split_wg)
       matvec_body<MT, LPR, U4, MODE, QK_TYPE_Q4_K, Q8IN>(a, 0, split_row, wg, split_wg, xq);
@@ -497,6 +518,12 @@ MatvecKernel matvec_kernel_for(int lpr, int mode, int type, bool q8in) {
     if (mode == 1) {
       if (type == QK_TYPE_Q4_K) return &matvec_kernel<MT, L, 1, QK_TYPE_Q4_K, false>;
       if (type == QK_TYPE_Q6_K) return &matvec_kernel<MT, L, 1, QK_TYPE_Q6_K, false>;
+      return nullptr;
+    }
+    if (mode == 2) {
+      if constexpr (MT != 1) return nullptr;
+      if (type == QK_TYPE_Q4_K) return &matvec_kernel<MT, L, 2, QK_TYPE_Q4_K, false>;
+      if (type == QK_TYPE_Q6_K) return &matvec_kernel<MT, L, 2, QK_TYPE_Q6_K, false>;
       return nullptr;
     }
     if (type == QK_TYPE_Q4_K) return &matvec_kernel<MT, L, 0, QK_TYPE_Q4_K, false>;

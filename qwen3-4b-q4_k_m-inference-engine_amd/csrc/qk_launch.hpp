@@ -33,11 +33,14 @@ struct MatvecParams {
   int32_t rows_total;           // rows of all segments (FFN mode: of gate)
   int32_t split_wg, split_row;  // mixed types: workgroups / rows of the Q4_K part
   int32_t pad;
+  void* argmax_ws;              // argmax mode: ArgmaxWorkspace (argmax.hpp)
+  uint32_t* argmax_result;      // argmax mode: index of the largest output
   MatvecSegment seg[kMaxSegments];
 };
 
 // mode 0: y_j = x . W_j^T for every segment (M <= 8);
-// mode 1: seg[0] = gate, seg[1] = up, h = SiLU(x . gate^T) * (x . up^T).
+// mode 1: seg[0] = gate, seg[1] = up, h = SiLU(x . gate^T) * (x . up^T);
+// mode 2: M = 1, one segment, y optional, *argmax_result = argmax of y.
 hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream);
 
 // Activation rows one launch_matvec can take for width K (its Q8 blocks live
@@ -59,6 +62,13 @@ hipError_t launch_gemm_prep(const float* x, int64_t M, int64_t K, void* workspac
 // y[M x N] = workspace . dequant(W)^T on MFMA, fp32 accumulation.
 hipError_t launch_gemm_core(const void* workspace, const void* w, int type, int64_t K, int64_t N,
                             float* y, int64_t M, hipStream_t stream);
+
+// Bytes of the argmax workspace (zero-filled once by the caller).
+size_t argmax_workspace_bytes();
+
+// *result = argmax of logits[0, count) with the reference's rules.
+hipError_t launch_argmax(const float* logits, int64_t count, void* workspace, uint32_t* result,
+                         hipStream_t stream);
 
 hipError_t launch_quantize_q8(const float* x, int64_t M, int64_t K, qk_q8_block* q8,
                               hipStream_t stream);

@@ -82,6 +82,21 @@ void silu_multiply(const float* gate, const float* up, float* output, size_t cou
                  "HIP kernel launch failed");
 }
 
+uint32_t argmax(const float* logits, size_t vocabulary_size) {
+    if (!logits || vocabulary_size == 0 || vocabulary_size > UINT32_MAX)
+        throw std::invalid_argument("Invalid argmax input");  // src/cuda/argmax.cu:73-74
+    const size_t ws_bytes = qk_argmax_workspace_size();
+    DeviceBuffer workspace(ws_bytes);
+    DeviceBuffer result(sizeof(uint32_t));
+    check_status(qk_memset_async(workspace.data, 0, ws_bytes, nullptr), "HIP memset failed");
+    check_status(qk_argmax(logits, static_cast<int64_t>(vocabulary_size),
+                           static_cast<uint32_t*>(result.data), workspace.data, ws_bytes, nullptr),
+                 "HIP kernel launch failed");
+    uint32_t index = 0;
+    check_status(qk_memcpy_d2h(&index, result.data, sizeof(index), nullptr), "HIP copy failed");
+    return index;
+}
+
 void dequantize_embeddings(const void* packed, float* output, size_t rows, size_t width,
                            size_t row_bytes, ggml_type type) {
     if (rows == 0) return;

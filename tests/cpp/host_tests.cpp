@@ -5,9 +5,11 @@
 // Nothing in this binary touches a device: every call below returns or
 // throws before the C-ABI reaches HIP.
 #include <cmath>
+#include <cstdint>
 #include <cstring>
 #include <filesystem>
 #include <fstream>
+#include <limits>
 #include <stdexcept>
 #include <vector>
 
@@ -64,6 +66,13 @@ TEST_CASE("dequantize_embeddings validation") {
     REQUIRE_THROWS_AS(kernels::dequantize_embeddings(nullptr, nullptr, 1, 2560, 1440, GGML_TYPE_F32),
                       std::invalid_argument);
     REQUIRE_NOTHROW(kernels::silu_multiply(nullptr, nullptr, nullptr, 0));
+}
+
+TEST_CASE("argmax rejects invalid input before touching the device") {
+    float x = 0;
+    REQUIRE_THROWS_AS(kernels::argmax(nullptr, 5), std::invalid_argument);  // argmax.cu:73-74
+    REQUIRE_THROWS_AS(kernels::argmax(&x, 0), std::invalid_argument);
+    REQUIRE_THROWS_AS(kernels::argmax(&x, size_t{UINT32_MAX} + 1), std::invalid_argument);
 }
 
 TEST_CASE("C-ABI status maps to the reference's exception types") {

@@ -5,10 +5,12 @@
 // around an offset output, zero input -> exact zeros. The expected values come
 // from the CPU oracle (oracle/qk_oracle.c).
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <filesystem>
 #include <fstream>
+#include <limits>
 #include <vector>
 
 #include "GGUF.hpp"
@@ -150,6 +152,21 @@ TEST_CASE("Matmul matches the quantized CPU reference across row counts") {
             for (size_t i = 0; i < expected.size(); ++i) REQUIRE(actual[i + 1] == 0.0f);
         }
     }
+}
+
+TEST_CASE("argmax returns the first index of the largest logit and ignores NaN") {
+    std::vector<float> logits(200000);
+    for (size_t i = 0; i < logits.size(); ++i) logits[i] = static_cast<float>((i * 7919) % 1000) * 0.5f;
+    logits[123457] = 1e6f;
+    logits[170001] = 1e6f;  // tie: the lower index wins
+    logits[9] = std::numeric_limits<float>::quiet_NaN();
+    DeviceBuffer d(logits.size() * sizeof(float));
+    kernels::detail::check_status(qk_memcpy_h2d(d.data, logits.data(), logits.size() * sizeof(float), nullptr), "copy");
+    REQUIRE(kernels::argmax(static_cast<const float*>(d.data), logits.size()) == 123457u);
+    std::vector<float> nothing(33, -std::numeric_limits<float>::infinity());
+    nothing[4] = std::numeric_limits<float>::quiet_NaN();
+    kernels::detail::check_status(qk_memcpy_h2d(d.data, nothing.data(), nothing.size() * sizeof(float), nullptr), "copy");
+    REQUIRE(kernels::argmax(static_cast<const float*>(d.data), nothing.size()) == 0xFFFFFFFFu);
 }
 
 TEST_CASE("Streams report readiness and moved-from streams throw") {

@@ -104,6 +104,24 @@ def test_other_validation(qk):
     assert lib.qk_ffn_gate_up(None, None, None, 12, 2560, 8, None, 1, None) == 1  # null pointers
 
 
+def test_argmax_validation_on_the_host(qk):
+    lib = qk.load()
+    n = lib.qk_argmax_workspace_size()
+    assert n >= 8 * 1024 + 4
+    p = ctypes.c_void_p(256)
+    assert lib.qk_argmax(None, 5, p, p, n, None) == 1           # null logits
+    assert lib.qk_argmax(p, 0, p, p, n, None) == 1              # empty
+    assert lib.qk_argmax(p, 1 << 32, p, p, n, None) == 1        # beyond uint32
+    assert lib.qk_argmax(p, 5, None, p, n, None) == 1           # null result
+    assert lib.qk_argmax(p, 5, p, p, n - 8, None) == 1          # small workspace
+    assert lib.qk_argmax(p, 5, p, ctypes.c_void_p(260), n, None) == 1  # misaligned workspace
+    assert b"argmax" in lib.qk_last_error()
+    assert lib.qk_matmul_argmax(p, p, 13, 2560, 8, None, p, p, n, None) == 2
+    assert lib.qk_matmul_argmax(p, p, 12, 2500, 8, None, p, p, n, None) == 1
+    assert lib.qk_matmul_argmax(p, p, 12, 2560, 8, None, None, p, n, None) == 1
+    assert lib.qk_matmul_argmax(None, p, 12, 2560, 8, None, p, p, n, None) == 1
+
+
 def test_cpp_host_layer_validation():
     """tests/cpp/host_tests.cpp: kernels::matmul throws the reference's exception types."""
     exe = ROOT / "qwen3-4b-q4_k_m-inference-engine_amd" / "_build" / "host_tests"

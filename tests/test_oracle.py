@@ -307,3 +307,19 @@ def test_silu_and_argmax(oracle):
     assert np.allclose(oracle.silu_multiply(g, u), ref, rtol=1e-6, atol=1e-7)
     v = np.array([1, 5, 3, 5, -1], np.float32)
     assert oracle.argmax(v) == 1
+
+
+def test_argmax_follows_the_reference_candidate_rules(oracle):
+    """src/cuda/argmax.cu: start (SIZE_MAX, -inf), replace on strictly greater,
+    lower index on ties; the uint32_t return turns SIZE_MAX into 0xFFFFFFFF."""
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    assert oracle.argmax(np.array([nan, 2, nan, 3, 3], np.float32)) == 3      # NaN never wins
+    assert oracle.argmax(np.array([-inf, -inf, -7], np.float32)) == 2        # -inf never wins
+    assert oracle.argmax(np.array([-inf, nan], np.float32)) == 0xFFFFFFFF    # nothing wins
+    assert oracle.argmax(np.array([], np.float32)) == 0xFFFFFFFF
+    assert oracle.argmax(np.array([-0.0, 0.0, -1], np.float32)) == 0         # -0 == +0: first
+    assert oracle.argmax(np.array([1, inf, inf], np.float32)) == 1
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        v = rng.integers(-3, 4, 1000).astype(np.float32)   # many ties
+        assert oracle.argmax(v) == int(np.argmax(v))       # numpy: first maximal index
