@@ -7,8 +7,10 @@
 //      values), scaled by a power of two 2^s that brings the row's largest
 //      |x| into [2^14, 2^15), then split into two fp16 planes hi + lo with
 //      hi = fp16(v), lo = fp16(v - hi): 22 significant bits of v.
-//   2. gemm_kernel: 128 x BN output tiles, 4 waves of 64 x BN/2, each a grid
-//      of v_mfma_f32_32x32x16_f16 tiles with fp32 accumulators. Per K-chunk
+//   2. gemm_kernel: 128 x BN output tiles, 8 waves: two K groups of 4 waves
+//      of 64 x BN/2 (alternate 16-deep steps, summed through LDS at the end),
+//      each a grid of v_mfma_f32_32x32x16_f16 tiles with fp32 accumulators,
+//      tiles dealt XCD by XCD so a weight tile stays in one L2. Per K-chunk
 //      of 32 weights (one scale group) the workgroup dequantises BN weight
 //      rows straight from the GGUF superblocks with the fp32 formula of
 //      src/cuda/embedding.cu:6-59, scaled by a per-row power of two 2^t
@@ -60,8 +62,37 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 
 // ---------------------------------------------------------------- prep ------
 
-// One workgroup per activation row. Pass 1: the row's max |x|. Pass 2: one
-// lane per 8 values, the 4 lanes of a quad holding one 32-value block.
+// Q8 round trip of one group of 8 activations (a quad of lanes holds one
+// 32-value block), scaled by `up`, split into fp16 hi/lo at hi + at, lo + at.
+__device__ __forceinline__ void prep_group(const f32x4 a, const f32x4 b, float up,
+                                           _Float16* __restrict__ hi, _Float16* __restrict__ lo,
+                                           int64_t at) {
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  float bmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) bmax = fmaxf(bmax, fabsf(v[i]));
+  bmax = fmaxf(bmax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                         0, __builtin_bit_cast(int, bmax), 0xB1, 0xF, 0xF, false)));
+  bmax = fmaxf(bmax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                         0, __builtin_bit_cast(int, bmax), 0x4E, 0xF, 0xF, false)));
+  const float scale = bmax / 127.0f;
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float c0 = bmax == 0.0f ? 0.0f : roundf((v[2 * i] / bmax) * 127.0f);
+    const float c1 = bmax == 0.0f ? 0.0f : roundf((v[2 * i + 1] / bmax) * 127.0f);
+    split2((c0 * scale) * up, (c1 * scale) * up, h[i], l[i]);
+  }
+  *reinterpret_cast<u32x4*>(hi + at) = u32x4{h[0], h[1], h[2], h[3]};
+  *reinterpret_cast<u32x4*>(lo + at) = u32x4{l[0], l[1], l[2], l[3]};
+}
+
+constexpr int kPrepGroups = 8;  // groups of 8 activations held per thread: K <= 16384 in one pass
+
+// One workgroup per activation row: the row's max |x| (for the power-of-two
+// scale), then the Q8 round trip of every 32-value block. Rows up to 16384
+// values stay in registers between the two steps; wider rows are read twice.
+// K % 32 == 0, so the 4 lanes of a quad are always in or out together.
 __global__ __launch_bounds__(256) void prep_rows_kernel(const float* __restrict__ x,
                                                         _Float16* __restrict__ hi,
                                                         _Float16* __restrict__ lo,
@@ -70,10 +101,28 @@ __global__ __launch_bounds__(256) void prep_rows_kernel(const float* __restrict_
   const int64_t row = blockIdx.x;
   const float* xr = x + row * K;
   const int tid = static_cast<int>(threadIdx.x);
+  const int groups = K / 8;
+  const bool resident = groups <= 256 * kPrepGroups;
+  f32x4 va[kPrepGroups], vb[kPrepGroups];
   float amax = 0.0f;
-  for (int i = 4 * tid; i < K; i += 1024) {
-    const f32x4 v = *reinterpret_cast<const f32x4_a4*>(xr + i);
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  if (resident) {
+#pragma unroll
+    for (int i = 0; i < kPrepGroups; ++i) {
+      const int g = tid + 256 * i;
+      va[i] = vb[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (g < groups) {
+        va[i] = *reinterpret_cast<const f32x4_a4*>(xr + 8 * g);
+        vb[i] = *reinterpret_cast<const f32x4_a4*>(xr + 8 * g + 4);
+      }
+      const f32x4 m4 = f32x4{fmaxf(fabsf(va[i].x), fabsf(vb[i].x)), fmaxf(fabsf(va[i].y), fabsf(vb[i].y)),
+                             fmaxf(fabsf(va[i].z), fabsf(vb[i].z)), fmaxf(fabsf(va[i].w), fabsf(vb[i].w))};
+      amax = fmaxf(amax, fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w)));
+    }
+  } else {
+    for (int i = 4 * tid; i < K; i += 1024) {
+      const f32x4 v = *reinterpret_cast<const f32x4_a4*>(xr + i);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
   }
   for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
   if ((tid & 63) == 0) partial[tid >> 6] = amax;
@@ -83,28 +132,16 @@ __global__ __launch_bounds__(256) void prep_rows_kernel(const float* __restrict_
   const float up = ldexpf(1.0f, s);
   if (tid == 0) row_scale[row] = ldexpf(1.0f, -s);
 
-  for (int g = tid; g < K / 8; g += 256) {  // K % 32 == 0: quads stay whole
-    const f32x4 a = *reinterpret_cast<const f32x4_a4*>(xr + 8 * g);
-    const f32x4 b = *reinterpret_cast<const f32x4_a4*>(xr + 8 * g + 4);
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    float bmax = 0.0f;
+  if (resident) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) bmax = fmaxf(bmax, fabsf(v[i]));
-    bmax = fmaxf(bmax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                           0, __builtin_bit_cast(int, bmax), 0xB1, 0xF, 0xF, false)));
-    bmax = fmaxf(bmax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                           0, __builtin_bit_cast(int, bmax), 0x4E, 0xF, 0xF, false)));
-    const float scale = bmax / 127.0f;
-    uint32_t h[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float c0 = bmax == 0.0f ? 0.0f : roundf((v[2 * i] / bmax) * 127.0f);
-      const float c1 = bmax == 0.0f ? 0.0f : roundf((v[2 * i + 1] / bmax) * 127.0f);
-      split2((c0 * scale) * up, (c1 * scale) * up, h[i], l[i]);
+    for (int i = 0; i < kPrepGroups; ++i) {
+      const int g = tid + 256 * i;
+      if (g < groups) prep_group(va[i], vb[i], up, hi, lo, row * K + 8 * g);
     }
-    const int64_t at = row * K + 8 * g;
-    *reinterpret_cast<u32x4*>(hi + at) = u32x4{h[0], h[1], h[2], h[3]};
-    *reinterpret_cast<u32x4*>(lo + at) = u32x4{l[0], l[1], l[2], l[3]};
+  } else {
+    for (int g = tid; g < groups; g += 256)
+      prep_group(*reinterpret_cast<const f32x4_a4*>(xr + 8 * g),
+                 *reinterpret_cast<const f32x4_a4*>(xr + 8 * g + 4), up, hi, lo, row * K + 8 * g);
   }
 }
 
@@ -179,10 +216,16 @@ __device__ __forceinline__ void store_split(const uint32_t (&hi)[BPT / 2],
                                             uint8_t* lds_row) {
   uint8_t* dh = lds_row + 2 * p * BPT;
   uint8_t* dl = dh + 2 * kBK;
+  if constexpr (BPT >= 8) {
 #pragma unroll
-  for (int i = 0; i < BPT / 8; ++i) {
-    reinterpret_cast<u32x4*>(dh)[i] = u32x4{hi[4 * i], hi[4 * i + 1], hi[4 * i + 2], hi[4 * i + 3]};
-    reinterpret_cast<u32x4*>(dl)[i] = u32x4{lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3]};
+    for (int i = 0; i < BPT / 8; ++i) {
+      reinterpret_cast<u32x4*>(dh)[i] = u32x4{hi[4 * i], hi[4 * i + 1], hi[4 * i + 2], hi[4 * i + 3]};
+      reinterpret_cast<u32x4*>(dl)[i] = u32x4{lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3]};
+    }
+  } else {
+    static_assert(BPT == 4, "4 or a multiple of 8 weights per thread");
+    *reinterpret_cast<uint2*>(dh) = make_uint2(hi[0], hi[1]);
+    *reinterpret_cast<uint2*>(dl) = make_uint2(lo[0], lo[1]);
   }
 }
 
@@ -242,43 +285,62 @@ struct GemmArgs {
   int M, N, K;
 };
 
+constexpr int kGemmWaves = 8;
+constexpr int kGemmThreads = 64 * kGemmWaves;
+
 template <int TYPE, int BN>
 struct GemmStage {
-  static constexpr int kTPR = 256 / BN;    // threads per weight row
-  static constexpr int kBPT = kBK / kTPR;  // weights per thread per chunk
-  u32x4 a[4];                              // 4 x 16 B of the activation planes
+  static constexpr int kTPR = kGemmThreads / BN;  // threads per weight row
+  static constexpr int kBPT = kBK / kTPR;         // weights per thread per chunk
+  u32x4 a[2];                                     // 2 x 16 B of the activation planes
   RawW<TYPE, kBPT> w;
 };
 
+// Tile t of the launch for workgroup b: consecutive tiles (the m-tiles of one
+// weight tile first) go to the same XCD (workgroups are dealt to the 8 XCDs
+// round-robin), so a weight tile is fetched into one L2 and reused there.
+__device__ __forceinline__ int xcd_tile(int b, int grid) {
+  const int per_xcd = grid / 8;  // grid is a multiple of 8
+  return (b % 8) * per_xcd + b / 8;
+}
+
+// 8 waves: waves 0-3 and 4-7 form two K groups that take alternate 16-deep
+// steps of every chunk on the same 128 x BN tile (each wave 64 x BN/2), so
+// every SIMD runs two waves; group 1's accumulators are added to group 0's
+// through LDS at the end (a fixed order: the result does not depend on timing).
 template <int TYPE, int BN>
-__global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
+__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs args, int tiles) {
   using Stage = GemmStage<TYPE, BN>;
   constexpr int kTPR = Stage::kTPR, kBPT = Stage::kBPT;
-  static_assert(kBPT >= 8, "dequant stores whole 16-byte pieces");
   constexpr int kNT = BN / 64;  // 32-wide MFMA tiles per wave along N
   constexpr int kBytes = TYPE == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes;
   constexpr int kStage = (kBM + BN) * kRowBytes;
+  static_assert(4 * 64 * 2 * kNT * 16 * 4 <= 2 * kStage, "reduction fits the stage buffers");
   __shared__ __align__(16) uint8_t lds[2 * kStage];
   __shared__ float col_scale[BN];
+  __shared__ float row_scale[kBM];
 
+  const int tile = xcd_tile(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  if (tile >= tiles) return;  // whole workgroup, before any barrier
   const int M = args.M, N = args.N, K = args.K;
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63, wave = tid >> 6;
+  const int kgroup = wave >> 2, wq = wave & 3;
   const int m_tiles = (M + kBM - 1) / kBM;
-  const int m0 = (static_cast<int>(blockIdx.x) % m_tiles) * kBM;
-  const int n0 = (static_cast<int>(blockIdx.x) / m_tiles) * BN;
-  const int wm = (wave & 1) * 64, wn = (wave >> 1) * (BN / 2);
+  const int m0 = (tile % m_tiles) * kBM;
+  const int n0 = (tile / m_tiles) * BN;
+  const int wm = (wq & 1) * 64, wn = (wq >> 1) * (BN / 2);
   const int nk = K / kBK;
   const int S = K / 256;
 
   // activation pieces: 16 B = 8 halves; piece (tid & 7) of a 128-byte LDS row
-  // image (hi 0..3, lo 4..7), rows (tid >> 3) + 32 i (clamped; never stored)
+  // image (hi 0..3, lo 4..7), rows (tid >> 3) + 64 i (clamped; never stored)
   const int a_piece = tid & 7;
   const _Float16* plane = (a_piece < 4 ? args.hi : args.lo) + (a_piece & 3) * 8;
-  const _Float16* a_src[4];
+  const _Float16* a_src[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    a_src[i] = plane + static_cast<int64_t>(min(m0 + (tid >> 3) + 32 * i, M - 1)) * K;
+  for (int i = 0; i < 2; ++i)
+    a_src[i] = plane + static_cast<int64_t>(min(m0 + (tid >> 3) + 64 * i, M - 1)) * K;
 
   const int w_local = tid / kTPR, w_part = tid % kTPR;
   const uint8_t* w_row = args.w + static_cast<int64_t>(min(n0 + w_local, N - 1)) * S * kBytes;
@@ -292,17 +354,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
   const int t = headroom_exponent(bound);
   const float wscale = ldexpf(1.0f, t);
   if (w_part == 0) col_scale[w_local] = ldexpf(1.0f, -t);
+  if (tid < kBM) row_scale[tid] = args.row_scale[min(m0 + tid, M - 1)];
 
   auto load_stage = [&](int kc, Stage& st) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st.a[i] = load16(a_src[i] + kc * kBK);
+    for (int i = 0; i < 2; ++i) st.a[i] = load16(a_src[i] + kc * kBK);
     load_raw<kBPT>(w_row, kc, w_part, st.w);
   };
   auto store_stage = [&](int kc, const Stage& st, int buf) {
     uint8_t* base = lds + buf * kStage;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<u32x4*>(base + ((tid >> 3) + 32 * i) * kRowBytes + a_piece * 16) = st.a[i];
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<u32x4*>(base + ((tid >> 3) + 64 * i) * kRowBytes + a_piece * 16) = st.a[i];
     dequant_store<kBPT>(st.w, kc, w_part, wscale, base + (kBM + w_local) * kRowBytes);
   };
 
@@ -312,55 +375,80 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
 #pragma unroll
     for (int j = 0; j < kNT; ++j) acc[i][j] = f32x16{};
 
+  // this wave's 16-deep step of the chunk (kgroup 0: k 0..15, 1: k 16..31)
   auto mma_chunk = [&](int buf) {
-    const uint8_t* base = lds + buf * kStage;
-    const int koff = 16 * (lane >> 5);  // bytes: 8 halves per half-wave
+    const uint8_t* base = lds + buf * kStage + kgroup * 32 + 16 * (lane >> 5);
+    half8 ah[2], al[2], bh[kNT], bl[kNT];
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      half8 ah[2], al[2], bh[kNT], bl[kNT];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const uint8_t* r = base + (wm + 32 * i + (lane & 31)) * kRowBytes + ks * 32 + koff;
-        ah[i] = *reinterpret_cast<const half8*>(r);
-        al[i] = *reinterpret_cast<const half8*>(r + 2 * kBK);
-      }
-#pragma unroll
-      for (int j = 0; j < kNT; ++j) {
-        const uint8_t* r = base + (kBM + wn + 32 * j + (lane & 31)) * kRowBytes + ks * 32 + koff;
-        bh[j] = *reinterpret_cast<const half8*>(r);
-        bl[j] = *reinterpret_cast<const half8*>(r + 2 * kBK);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < kNT; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
-        }
+    for (int i = 0; i < 2; ++i) {
+      const uint8_t* r = base + (wm + 32 * i + (lane & 31)) * kRowBytes;
+      ah[i] = *reinterpret_cast<const half8*>(r);
+      al[i] = *reinterpret_cast<const half8*>(r + 2 * kBK);
     }
+#pragma unroll
+    for (int j = 0; j < kNT; ++j) {
+      const uint8_t* r = base + (kBM + wn + 32 * j + (lane & 31)) * kRowBytes;
+      bh[j] = *reinterpret_cast<const half8*>(r);
+      bl[j] = *reinterpret_cast<const half8*>(r + 2 * kBK);
+    }
+    // one product term over every tile before the next term, so each
+    // accumulator's dependent MFMAs are 2*kNT issues apart
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < kNT; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < kNT; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < kNT; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
   };
 
-  // prologue: chunk 0 into LDS, chunk 1 in registers (nk >= 8)
-  Stage s0, s1;
-  load_stage(0, s0);
-  load_stage(1, s1);
-  store_stage(0, s0, 0);
+  // A ring of kDepth register stages keeps the global loads kDepth-1 chunks
+  // ahead of their dequantisation (HBM latency is several chunk times); two
+  // LDS buffers alternate. Step c: load chunk c+kDepth into the stage chunk c
+  // vacated, multiply chunk c from LDS, dequantise and store chunk c+1 into
+  // the other buffer, barrier. Loads past the end re-read the last chunk (in
+  // bounds, unused) so no load sits under a branch. nk is a multiple of 8.
+  constexpr int kDepth = 4;
+  Stage st[kDepth];
+#pragma unroll
+  for (int i = 0; i < kDepth; ++i) load_stage(i, st[i]);
+  store_stage(0, st[0], 0);
   __syncthreads();
-  // two chunks per trip so the register stages stay static: consume chunk kc
-  // from LDS while chunk kc+2 loads and chunk kc+1 is dequantised and stored
-  for (int kc = 0; kc < nk; kc += 2) {
-    if (kc + 2 < nk) load_stage(kc + 2, s0);
-    mma_chunk(0);
-    store_stage(kc + 1, s1, 1);  // nk even
-    __syncthreads();
-    if (kc + 3 < nk) load_stage(kc + 3, s1);
-    mma_chunk(1);
-    if (kc + 2 < nk) store_stage(kc + 2, s0, 0);
-    __syncthreads();
+  for (int kc = 0; kc < nk; kc += kDepth) {
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      const int c = kc + i;
+      load_stage(min(c + kDepth, nk - 1), st[i]);
+      mma_chunk(i & 1);
+      if (c + 1 < nk) store_stage(c + 1, st[(i + 1) % kDepth], (i + 1) & 1);
+      __syncthreads();
+    }
   }
 
+  // K group 1 hands its partial tile to group 0 (lane-major so the stores and
+  // loads of a wave are contiguous)
+  float* red = reinterpret_cast<float*>(lds) + wq * (2 * kNT * 16 * 64);
+  if (kgroup == 1) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < kNT; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[((i * kNT + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+  }
+  __syncthreads();
+  if (kgroup == 1) return;
+
   // epilogue: D lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, column l%32
+  float* __restrict__ y = args.y;
 #pragma unroll
   for (int j = 0; j < kNT; ++j) {
     const int nl = wn + 32 * j + (lane & 31);
@@ -371,8 +459,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < M && n < N)
-          args.y[static_cast<int64_t>(m) * N + n] = (acc[i][j][r] * args.row_scale[m]) * cs;
+        const float v = acc[i][j][r] + red[((i * kNT + j) * 16 + r) * 64 + lane];
+        if (m < M && n < N) y[static_cast<int64_t>(m) * N + n] = (v * row_scale[m - m0]) * cs;
       }
   }
 }
@@ -380,14 +468,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmArgs args) {
 template <int TYPE>
 hipError_t launch_gemm_type(const GemmArgs& a, hipStream_t stream) {
   const int m_tiles = (a.M + kBM - 1) / kBM;
-  // 128-wide weight tiles when they still give a workgroup per CU, else 64
-  if (static_cast<int64_t>(m_tiles) * ((a.N + 127) / 128) >= 256) {
-    const uint32_t grid = static_cast<uint32_t>(m_tiles * ((a.N + 127) / 128));
-    gemm_kernel<TYPE, 128><<<grid, 256, 0, stream>>>(a);
-  } else {
-    const uint32_t grid = static_cast<uint32_t>(m_tiles * ((a.N + 63) / 64));
-    gemm_kernel<TYPE, 64><<<grid, 256, 0, stream>>>(a);
-  }
+  // 128-wide weight tiles when they still give a workgroup per CU, else 64;
+  // the grid is rounded up to a multiple of the 8 XCDs (extra workgroups exit)
+  const bool wide = static_cast<int64_t>(m_tiles) * ((a.N + 127) / 128) >= 256;
+  const int tiles = m_tiles * ((a.N + (wide ? 127 : 63)) / (wide ? 128 : 64));
+  const uint32_t grid = static_cast<uint32_t>((tiles + 7) / 8 * 8);
+  if (wide)
+    gemm_kernel<TYPE, 128><<<grid, kGemmThreads, 0, stream>>>(a, tiles);
+  else
+    gemm_kernel<TYPE, 64><<<grid, kGemmThreads, 0, stream>>>(a, tiles);
   return hipGetLastError();
 }
 
