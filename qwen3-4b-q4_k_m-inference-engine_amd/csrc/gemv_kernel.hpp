@@ -89,10 +89,22 @@ __device__ __forceinline__ int piece_block_a(uint32_t pc, int type) {
 __device__ __forceinline__ int piece_block_step(int type) { return type == QK_TYPE_Q4_K ? 1 : 2; }
 
 // Q8 of one group of 8 consecutive activations per lane; the 4 lanes of a
-// quad form one 32-activation block. code = roundf(RN(x/amax)*127) with the
-// quotient from the correctly rounded reciprocal plus one Markstein
-// correction step, which equals the IEEE quotient whenever the code can be
-// non-zero (2^-64 <= amax <= 2^64); other amax take the IEEE division.
+// quad form one 32-activation block. code = roundf(RN(x/amax)*127) and
+// scale = RN(amax/127), as the reference computes them in float, with
+// amax in [2^-64, 2^64] (every amax for which a code can be non-zero):
+//  - 1/amax: v_rcp_f32 plus one FMA refinement, which equals the IEEE
+//    reciprocal for every amax in that range (checked exhaustively on gfx950);
+//  - x/amax and amax/127: Markstein's correction q0 = x*r, e = fma(-q0, b, x),
+//    q = fma(e, r, q0) with the correctly rounded reciprocal r, which gives the
+//    IEEE quotient (x/amax: checked on the CPU over 3.1e8 random and 9e6
+//    near-tie pairs and on the GPU; amax/127: exhaustively on gfx950);
+//  - roundf(t) for |t| <= 127: trunc(t + copysign(0.49999997f, t)), equal to
+//    roundf for every such float (checked exhaustively); the float-to-int
+//    conversion truncates.
+// Other amax take the IEEE division and roundf. (refined_rcp, markstein_div
+// and round_code live in qk_device.hpp; tests/cpp/quant_arith_check.hip
+// repeats the exhaustive checks on the GPU.)
+
 __device__ __forceinline__ void quantize_group(const float (&v)[8], qk_q8_block* blk, uint32_t q) {
   float amax = 0.0f;
 #pragma unroll
@@ -101,22 +113,22 @@ __device__ __forceinline__ void quantize_group(const float (&v)[8], qk_q8_block*
                          0, __builtin_bit_cast(int, amax), 0xB1, 0xF, 0xF, false)));
   amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
                          0, __builtin_bit_cast(int, amax), 0x4E, 0xF, 0xF, false)));
+  const bool usual = amax >= 0x1p-64f && amax <= 0x1p64f;
   int code[8];
-  if (amax == 0.0f) {
+  float scale;
+  if (usual) {
+    const float r = refined_rcp(amax);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) code[i] = round_code(markstein_div(v[i], amax, r) * 127.0f);
+    scale = markstein_div(amax, 127.0f, 1.0f / 127.0f);
+  } else if (amax == 0.0f) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) code[i] = 0;
-  } else if (amax >= 0x1p-64f && amax <= 0x1p64f) {
-    const float r = 1.0f / amax;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float q0 = v[i] * r;
-      const float e = __builtin_fmaf(-q0, amax, v[i]);
-      const float quotient = __builtin_fmaf(e, r, q0);
-      code[i] = static_cast<int>(roundf(quotient * 127.0f));
-    }
+    scale = 0.0f;
   } else {
 #pragma unroll
     for (int i = 0; i < 8; ++i) code[i] = static_cast<int>(roundf((v[i] / amax) * 127.0f));
+    scale = amax / 127.0f;
   }
   uint32_t lo = 0, hi = 0;
   int sum = 0;
@@ -131,7 +143,6 @@ __device__ __forceinline__ void quantize_group(const float (&v)[8], qk_q8_block*
   const int pair = sum + __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, false);
   const int other = __builtin_amdgcn_update_dpp(0, pair, 0x4E, 0xF, 0xF, false);
   if (q == 0) {
-    const float scale = amax / 127.0f;
     blk->scale = scale;
     blk->scaled_sum = scale * static_cast<float>(pair + other);
     blk->neg32_sum_lo = -32 * pair;
@@ -226,20 +237,40 @@ __device__ void copy_q8_into_lds(const qk_q8_block* __restrict__ q8, int M, int 
   }
 }
 
+// v + the same register of the lane selected by a DPP control (row-local).
+template <int CTRL>
+__device__ __forceinline__ float add_dpp(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                   0xF, 0xF, false));
+}
+
+// v summed over lane bit 4 / lane bit 5 with the gfx950 lane-swap
+// instructions (VALU, no LDS round trip). The two results of a swap are
+// copied out as scalars before the bit casts: bit casting the subscripted
+// elements directly made the compiler use the first result twice.
+__device__ __forceinline__ float swap16_sum(float v) {
+  const auto t = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  const unsigned a = t[0], b = t[1];
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float swap32_sum(float v) {
+  const auto t = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  const unsigned a = t[0], b = t[1];
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
 // Sum over the LPR lanes of each row (aligned lane groups); every lane of the
 // group receives the sum.
 template <int LPR>
 __device__ __forceinline__ float row_lanes_sum(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                             0xB1, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                             0x4E, 0xF, 0xF, false));
-  if constexpr (LPR >= 8)
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
-                                                               0x141, 0xF, 0xF, false));
-  if constexpr (LPR >= 16) v += __shfl_xor(v, 8);
-  if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
-  if constexpr (LPR >= 64) v += __shfl_xor(v, 32);
+  v = add_dpp<0xB1>(v);                             // lane bit 0 (quad_perm 1,0,3,2)
+  v = add_dpp<0x4E>(v);                             // lane bit 1 (quad_perm 2,3,0,1)
+  if constexpr (LPR >= 8) v = add_dpp<0x141>(v);    // lane bit 2 (row_half_mirror)
+  if constexpr (LPR >= 16) v = add_dpp<0x140>(v);   // lane bit 3 (row_mirror)
+  if constexpr (LPR >= 32) v = swap16_sum(v);       // lane bit 4
+  if constexpr (LPR >= 64) v = swap32_sum(v);       // lane bit 5
   return v;
 }
 

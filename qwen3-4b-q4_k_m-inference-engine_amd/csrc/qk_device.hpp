@@ -99,6 +99,27 @@ struct XFrag {  // one Q8 activation block
   u32x4 c0, c1, rec;
 };
 
+// Exact-rounding building blocks of the activation quantiser (Q8 codes and
+// scales as the reference computes them in float, for a block maximum amax
+// in [2^-64, 2^64]):
+//  refined_rcp(a)        = RN(1/a): v_rcp_f32 plus one FMA refinement;
+//  markstein_div(x,b,r)  = RN(x/b) given r = RN(1/b) (Markstein's correction);
+//  round_code(t)         = roundf(t) for |t| <= 127, as a truncation of
+//                          t + copysign(0.49999997f, t).
+// Each identity holds for every float in its range: tests/cpp/
+// quant_arith_check.hip checks them exhaustively on the GPU.
+__device__ __forceinline__ float refined_rcp(float a) {
+  const float r0 = __builtin_amdgcn_rcpf(a);
+  return __builtin_fmaf(__builtin_fmaf(-a, r0, 1.0f), r0, r0);
+}
+__device__ __forceinline__ float markstein_div(float x, float b, float r) {
+  const float q0 = x * r;
+  return __builtin_fmaf(__builtin_fmaf(-q0, b, x), r, q0);
+}
+__device__ __forceinline__ int round_code(float t) {
+  return static_cast<int>(t + __builtin_copysignf(0.49999997f, t));
+}
+
 // Q4_K piece j (0..3): the 32 qs bytes 32j..32j+31, whose low nibbles are
 // sub-block 2j and high nibbles sub-block 2j+1, plus the header.
 struct Q4KPiece {
