@@ -98,8 +98,17 @@ int matvec_rows_per_launch(int64_t K) {
 }
 
 hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
+  // M = 1 shapes whose per-CU share fits in LDS take the whole-share kernel
+  // (gemv_stream.hip); QK_NO_STREAM_MATVEC builds keep every shape here.
+#ifndef QK_NO_STREAM_MATVEC
+  bool launched = false;
+  hipError_t e = launch_stream_matvec(p, mode, stream, launched);
+  if (e != hipSuccess || launched) return e;
+#else
+  hipError_t e = hipSuccess;
+#endif
   DeviceFacts dev;
-  hipError_t e = device_facts(dev);
+  e = device_facts(dev);
   if (e != hipSuccess) return e;
   const int M = p.M;
   const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;

@@ -105,7 +105,7 @@ __device__ __forceinline__ int piece_block_step(int type) { return type == QK_TY
 // and round_code live in qk_device.hpp; tests/cpp/quant_arith_check.hip
 // repeats the exhaustive checks on the GPU.)
 
-__device__ __forceinline__ void quantize_group(const float (&v)[8], qk_q8_block* blk, uint32_t q) {
+__device__ __forceinline__ void quantize_group(const float (&v)[8], lds_q8_block* blk, uint32_t q) {
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -138,7 +138,7 @@ __device__ __forceinline__ void quantize_group(const float (&v)[8], qk_q8_block*
     hi |= (static_cast<uint32_t>(code[i + 4]) & 0xFFu) << (8 * i);
     sum += code[i] + code[i + 4];
   }
-  *reinterpret_cast<uint2*>(blk->codes + 8 * q) = make_uint2(lo, hi);
+  *reinterpret_cast<lds_u32x2*>(blk->codes + 8 * q) = u32x2{lo, hi};
   // lanes 0,1 of the quad hold codes 0..15, lanes 2,3 codes 16..31
   const int pair = sum + __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, false);
   const int other = __builtin_amdgcn_update_dpp(0, pair, 0x4E, 0xF, 0xF, false);
@@ -194,7 +194,7 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int M, int 
 }
 
 __device__ __forceinline__ void quantize_task(f32x4 a, f32x4 b, bool zero, int t,
-                                              qk_q8_block* __restrict__ lds) {
+                                              lds_q8_block* lds) {
   if (zero) {
     a = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     b = a;
@@ -207,8 +207,8 @@ __device__ __forceinline__ void quantize_task(f32x4 a, f32x4 b, bool zero, int t
 // K/8 and 64*nq are multiples of 4, so the 4 lanes of a quad are always in
 // or out together.
 template <int MT>
-__device__ void quantize_into_lds(const float* __restrict__ x, int M, int K, int nq,
-                                  const XStage<MT>& st, qk_q8_block* __restrict__ lds) {
+__device__ __forceinline__ void quantize_staged_into_lds(int M, int K, int nq, const XStage<MT>& st,
+                                                         lds_q8_block* lds) {
   const int groups = K / 8;
   const int tasks = MT * groups;
   const int step = 64 * nq;
@@ -217,6 +217,15 @@ __device__ void quantize_into_lds(const float* __restrict__ x, int M, int K, int
     const int t = static_cast<int>(threadIdx.x) + step * i;
     if (t < tasks) quantize_task(st.a[i], st.b[i], t / groups >= M, t, lds);
   }
+}
+
+template <int MT>
+__device__ void quantize_into_lds(const float* __restrict__ x, int M, int K, int nq,
+                                  const XStage<MT>& st, lds_q8_block* lds) {
+  quantize_staged_into_lds<MT>(M, K, nq, st, lds);
+  const int groups = K / 8;
+  const int tasks = MT * groups;
+  const int step = 64 * nq;
   for (int t = static_cast<int>(threadIdx.x) + step * kXStaged; t < tasks; t += step) {
     f32x4 a, b;
     load_x_group(x, M, K, t, a, b);
@@ -227,10 +236,10 @@ __device__ void quantize_into_lds(const float* __restrict__ x, int M, int K, int
 // Caller-provided Q8 blocks [M][K/32] -> LDS [MT][K/32]; rows m >= M are zero.
 template <int MT>
 __device__ void copy_q8_into_lds(const qk_q8_block* __restrict__ q8, int M, int K,
-                                 qk_q8_block* __restrict__ lds) {
+                                 lds_q8_block* lds) {
   const int per_row = (K / 32) * 3;  // 16-byte chunks
   const u32x4* src = reinterpret_cast<const u32x4*>(q8);
-  u32x4* dst = reinterpret_cast<u32x4*>(lds);
+  lds_u32x4* dst = reinterpret_cast<lds_u32x4*>(lds);
   for (int t = threadIdx.x; t < MT * per_row; t += 64 * matvec_waves<MT>()) {
     const int m = t / per_row;
     dst[t] = m < M ? src[t] : u32x4{0u, 0u, 0u, 0u};
@@ -296,7 +305,7 @@ struct MatvecArgs {
 // Returns the thread's best argmax key (argmax mode; 0 otherwise).
 template <int MT, int LPR, int U, int MODE, int TYPE, bool Q8IN>
 __device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo, int row_hi, int wg,
-                                                int nwg, qk_q8_block* __restrict__ xq) {
+                                                int nwg, lds_q8_block* xq) {
   using Piece = typename PieceOf<TYPE>::type;
   constexpr int kRPU = 64 / LPR;  // rows per group
   constexpr int kSPI = LPR / 4;   // superblocks per iteration
@@ -400,10 +409,14 @@ __device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo,
         const int phase = MODE == 1 && cc.k >= ipu;
         const int kk = phase ? cc.k - ipu : cc.k;
         const int s_raw = kk * kSPI + sbo;
-        const int blk = min(s_raw, S - 1) * 8 + blk_a;
+        // LDS block index (< 2^16: the blocks fit in LDS). The mask lets the
+        // compiler form the address with a 24-bit multiply-add; a 32-bit one
+        // became v_mad_u64_u32 with an unrelated register as its high half,
+        // and a wait for that register's pending weight load.
+        const int blk = (min(s_raw, S - 1) * 8 + blk_a) & 0xFFFF;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          const qk_q8_block* xr = xq + m * S * 8 + blk;
+          const lds_q8_block* xr = xq + m * S * 8 + blk;
           const float v = dot_piece<TYPE>(f[i], load_x(xr), load_x(xr + blk_step), pc, TYPE);
           const float add = s_raw < S ? v : 0.0f;
           if (phase) up[m] += add;
@@ -455,6 +468,14 @@ __device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo,
   // further, and every consume follows its own issue sequence in the code, so
   // the wait before it counts exactly the loads issued after its buffer.
   const int nchunks = (T + U - 1) / U;
+#ifdef QK_MATVEC_SINGLE
+  consume(fa, 0);
+  for (int chunk = 1; chunk < nchunks; ++chunk) {
+    issue(ci, fa);
+    consume(fa, chunk * U);
+  }
+  return best_key;
+#endif
   for (int chunk = 0; chunk < nchunks;) {
     if (chunk + 1 == nchunks) {
       consume(fa, chunk * U);
@@ -485,7 +506,7 @@ __device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo,
 template <int MT, int LPR, int MODE, int TYPE, bool Q8IN>
 __global__ __launch_bounds__(64 * matvec_waves<MT>()) void matvec_kernel(const MatvecParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  qk_q8_block* xq = reinterpret_cast<qk_q8_block*>(lds_raw);
+  lds_q8_block* xq = (lds_q8_block*)(lds_raw);
   constexpr int U4 = QK_MATVEC_U4, U6 = QK_MATVEC_U6;
 
   MatvecArgs a;

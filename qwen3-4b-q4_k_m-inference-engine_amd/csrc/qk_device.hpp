@@ -142,11 +142,22 @@ struct Q6KPiece {
   uint32_t shift;    // field misalignment in bits: 0 or 16
 };
 
-__device__ __forceinline__ XFrag load_x(const qk_q8_block* __restrict__ xb) {
+// Q8 activation blocks in LDS, addressed through 32-bit local pointers. (With
+// generic pointers the compiler formed 64-bit LDS addresses whose unused high
+// half was some other register, and then waited for that register's pending
+// global load before the LDS read: a false dependency that serialised the
+// weight stream.)
+typedef __attribute__((address_space(3))) qk_q8_block lds_q8_block;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+
+__device__ __forceinline__ XFrag load_x(const lds_q8_block* xb) {
+  const lds_u32x4* p = reinterpret_cast<const lds_u32x4*>(xb);
   XFrag f;
-  f.c0 = load16(xb->codes);
-  f.c1 = load16(xb->codes + 16);
-  f.rec = load16(&xb->scale);
+  f.c0 = p[0];  // codes 0..15
+  f.c1 = p[1];  // codes 16..31
+  f.rec = p[2];  // scale, scaled_sum, neg32_sum_lo, neg32_sum_hi
   return f;
 }
 

@@ -43,6 +43,11 @@ struct MatvecParams {
 // mode 2: M = 1, one segment, y optional, *argmax_result = argmax of y.
 hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream);
 
+// The whole-share mat-vec for M = 1 (gemv_stream.hip): launched (and
+// `launched` set) when every workgroup's share of the weights fits in LDS;
+// otherwise nothing is enqueued and launch_matvec uses the streaming kernel.
+hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
+
 // Activation rows one launch_matvec can take for width K (its Q8 blocks live
 // in LDS): 8, 4, 2 or 1, or 0 when even one row does not fit.
 int matvec_rows_per_launch(int64_t K);

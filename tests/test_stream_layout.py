@@ -1,0 +1,132 @@
+"""CPU model of the whole-share mat-vec's work split and addressing
+(qwen3-4b-q4_k_m-inference-engine_amd/csrc/gemv_stream.hip, gemv_stream.hpp):
+for each shape, every global read, LDS write, piece read, Q8-block read and
+superblock-sum index of every lane of every wave of every workgroup is checked
+against its buffer, and every superblock of every row is shown to be covered
+exactly once. The model restates the launcher's and kernel's integer arithmetic
+(its own code, vectorised over workgroups, waves and lanes); a change to either
+file must be mirrored here."""
+import numpy as np
+import pytest
+
+CUS, MAX_LDS, WAVES, MAX_J, XSTAGED = 256, 160 * 1024, 16, 8, 2
+BYTES = {12: 144, 14: 210}
+MAX_K = 8 * 64 * WAVES * XSTAGED
+
+
+def launcher(rows, types, K, mode):
+    """(workgroups per segment, J, max_sb, lds bytes) or None when the streaming kernel is used."""
+    S = K // 256
+    if K > MAX_K:
+        return None
+    nseg = 1 if mode == 1 else len(rows)
+    parts = 2 if mode == 1 else 1
+    wpp = WAVES // parts
+    byt = [rows[j] * S * BYTES[types[j]] * parts for j in range(nseg)]
+    total = float(sum(byt))
+    count = [min(max(int(CUS * b / total + 0.5), 1), rows[j]) for j, b in enumerate(byt)]
+    while sum(count) > CUS:
+        count[count.index(max(count))] -= 1
+    J, max_sb = 0, 0
+    for j in range(nseg):
+        rows_max = -(-rows[j] // count[j])
+        sb = rows_max * S
+        wave_bytes = 2 + -(-sb // wpp) * BYTES[types[j]]
+        J = max(J, min(-(-(-(-wave_bytes // 16)) // 64), MAX_J + 1))
+        max_sb = max(max_sb, sb)
+    if J > MAX_J:
+        return None
+    lds = S * 8 * 48 + WAVES * J * 1024 + parts * max_sb * 4
+    if lds > MAX_LDS:
+        return None
+    return count, J, max_sb, lds
+
+
+def check_shape(rows, types, K, mode, bases):
+    cfg = launcher(rows, types, K, mode)
+    if cfg is None:
+        return False
+    count, J, max_sb, lds = cfg
+    S = K // 256
+    parts = 2 if mode == 1 else 1
+    wpp = WAVES // parts
+    nseg = 1 if mode == 1 else len(rows)
+    seen = [np.zeros((parts, rows[j] * S), np.int64) for j in range(nseg)]
+    wave = np.arange(WAVES)[:, None, None]
+    lane = np.arange(64)[None, :, None]
+    jj = np.arange(J)[None, None, :]
+    for j in range(nseg):
+        B = BYTES[types[j]]
+        rb = S * B
+        per, rem = rows[j] // count[j], rows[j] % count[j]
+        for g in range(count[j]):
+            r0 = g * per + min(g, rem)
+            r1 = r0 + per + (1 if g < rem else 0)
+            assert 0 <= r0 < r1 <= rows[j]
+            nsb = (r1 - r0) * S
+            assert nsb <= max_sb
+            part, wv = wave // wpp, wave % wpp
+            sb_a, sb_b = nsb * wv // wpp, nsb * (wv + 1) // wpp
+            base = np.where(part == 1, bases[1] if mode == 1 else 0, bases[j])
+            run = base + r0 * rb + np.where(sb_b > sb_a, sb_a, 0) * B
+            o = run & 3
+            if types[j] == 12:
+                assert np.all(run % 16 == 0)
+            run4 = run - o
+            L = np.maximum((o + (sb_b - sb_a) * B + 15) >> 4, 1)
+            end = base + rows[j] * rb
+            last = base + ((rows[j] * rb + 3) & ~3) - 16
+            c = np.minimum(lane + 64 * jj, L - 1)
+            a = np.minimum(run4 + 16 * c, last)
+            # global reads: 16 bytes inside the matrix's dwords, dword aligned
+            assert np.all(a >= base) and np.all(a + 16 <= ((end + 3) & ~3)) and np.all(a % 4 == 0)
+            off = a - run4
+            # LDS writes inside the wave's region
+            assert np.all(off >= 0) and np.all(off + 16 <= J * 1024)
+            # the written bytes cover the run: chunk c < L-1 unmoved, so [0, 16(L-1)) and the last chunk
+            cov_end = np.maximum(16 * (L - 1), np.minimum(16 * (L - 1), last - run4) + 16)
+            assert np.all(cov_end >= o + (sb_b - sb_a) * B)
+            # pieces: superblock offsets and Q6_K field reads inside the superblock
+            for w in range(WAVES):
+                a_, b_ = int(sb_a[w, 0, 0]), int(sb_b[w, 0, 0])
+                seen[j][int(part[w, 0, 0]), r0 * S + a_: r0 * S + b_] += 1
+                q = np.arange(4 * (b_ - a_))
+                s = (a_ + (q >> 2)) % S
+                pc = q & 3
+                blk = s * 8 + np.where(types[j] == 12, 2 * pc, 4 * (pc >> 1) + (pc & 1))
+                step = 1 if types[j] == 12 else 2
+                assert np.all(blk + step < S * 8)
+                assert np.all(int(part[w, 0, 0]) * max_sb + a_ + (q >> 2) < parts * max_sb)
+    for j in range(nseg):
+        assert np.all(seen[j] == 1), "every superblock of every row exactly once"
+    assert lds <= MAX_LDS
+    return True
+
+
+SHAPES = [
+    ([2560], [14], 9728, 0),             # ffn_down / config 1
+    ([9728], [12], 2560, 0),             # config 0
+    ([9728, 9728], [12, 12], 2560, 1),   # gate + up
+    ([2560], [12], 4096, 0),             # attn_output
+    ([4096, 1024, 1024], [12, 12, 14], 2560, 0),  # q/k/v
+    ([3, 1, 2], [12, 12, 14], 256, 0),
+    ([1], [14], 256, 0),
+    ([5], [14], 2560, 0),
+    ([101], [12], 3328, 0),
+    ([101], [14], 9728, 0),
+    ([1000], [14], 2560, 0),
+    ([64], [14], 9728, 0),
+    ([5, 5], [14, 14], 2560, 1),
+    ([257], [14], 768, 0),
+]
+
+
+@pytest.mark.parametrize("rows,types,K,mode", SHAPES)
+def test_whole_share_indices_in_bounds(rows, types, K, mode):
+    # Q6_K bases only 4-byte aligned; Q4_K bases 16-byte aligned (the C-ABI's rules)
+    bases = [(1 << 24) * (i + 1) + (4 if t == 14 else 0) for i, t in enumerate(types)]
+    assert check_shape(rows, types, K, mode, bases)
+
+
+def test_lm_head_takes_the_streaming_kernel():
+    assert launcher([151936], [14], 2560, 0) is None
