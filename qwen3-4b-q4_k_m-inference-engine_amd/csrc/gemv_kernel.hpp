@@ -468,14 +468,6 @@ __device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo,
   // further, and every consume follows its own issue sequence in the code, so
   // the wait before it counts exactly the loads issued after its buffer.
   const int nchunks = (T + U - 1) / U;
-#ifdef QK_MATVEC_SINGLE
-  consume(fa, 0);
-  for (int chunk = 1; chunk < nchunks; ++chunk) {
-    issue(ci, fa);
-    consume(fa, chunk * U);
-  }
-  return best_key;
-#endif
   for (int chunk = 0; chunk < nchunks;) {
     if (chunk + 1 == nchunks) {
       consume(fa, chunk * U);
