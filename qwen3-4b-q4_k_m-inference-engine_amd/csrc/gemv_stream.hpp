@@ -269,7 +269,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
     const uint8_t* a = run4 + 16 * c;
     a = a < last ? a : last;
     ws.off[jj] = static_cast<int>(a - run4);
-    ws.chunk[jj] = load16_a4(a);
+    ws.chunk[jj] = stream_load16_a4(a);
   }
   __builtin_amdgcn_sched_barrier(0);
 

@@ -43,6 +43,16 @@ __device__ __forceinline__ uint32_t load_u32(const void* p) {
   return *reinterpret_cast<const uint32_t*>(p);
 }
 
+// The same loads with the nontemporal hint, for weight bytes that a kernel
+// reads exactly once (one instruction per byte): the streamed matrix then does
+// not push code, activations and other reused lines out of the caches
+// (whole-share mat-vec: 3-5% per decode launch). Not for bytes that several
+// instructions read (the streaming mat-vec's pieces share cache lines: there
+// the hint made lm_head 2x slower).
+__device__ __forceinline__ u32x4 stream_load16_a4(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(p));
+}
+
 // fp16 bits -> fp32 (exact, subnormals kept: the kernels run with fp16
 // denormals enabled, which is the gfx950 default mode).
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
