@@ -8,9 +8,12 @@
 #include <mutex>
 #include <utility>
 
-#include "gemv_stream.hpp"
+#include "gemv_stream_mt.hpp"
 
 namespace qk {
+
+StreamMtKernel stream_mt_kernel_m4(int type, int J, int mode);
+StreamMtKernel stream_mt_kernel_m8(int type, int J, int mode);
 
 namespace {
 
@@ -42,7 +45,7 @@ StreamKernel stream_kernel(int type, int J, int mode) {
 
 std::mutex g_mutex;
 std::map<int, std::pair<int, int>> g_device;        // device -> (CUs, LDS bytes per workgroup)
-std::map<std::pair<StreamKernel, int>, bool> g_lds;  // dynamic LDS limit set
+std::map<std::pair<const void*, int>, bool> g_lds;  // dynamic LDS limit set
 
 hipError_t device_limits(int& cus, int& max_lds) {
   int device = 0;
@@ -63,39 +66,27 @@ hipError_t device_limits(int& cus, int& max_lds) {
   return hipSuccess;
 }
 
-hipError_t allow_lds(StreamKernel fn, int lds) {
+hipError_t allow_lds(const void* fn, int lds) {
   std::lock_guard<std::mutex> lock(g_mutex);
   const auto key = std::make_pair(fn, lds);
   if (g_lds.count(key)) return hipSuccess;
-  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   if (e == hipSuccess) g_lds.emplace(key, true);
   return e;
 }
 
 int type_bytes(int type) { return type == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes; }
 
-}  // namespace
-
-hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t stream, bool& launched) {
-  launched = false;
-  if (p.M != 1 || p.x == nullptr || (mode != 0 && mode != 1) || p.K > kStreamMaxK) return hipSuccess;
-  int cus = 0, max_lds = 0;
-  hipError_t e = device_limits(cus, max_lds);
-  if (e != hipSuccess) return e;
-  const int nseg = mode == 1 ? 1 : p.nseg;
-  const int parts = mode == 1 ? 2 : 1, wpp = kStreamWaves / parts;
-  const int64_t S = p.S;
-
-  // Workgroups per segment in proportion to bytes, at least one, at most one
-  // per row, and no more than one per CU in all.
+// Workgroups per segment in proportion to bytes, at least one, at most one
+// per row, and no more than one per CU in all; false if segments outnumber CUs.
+bool workgroup_counts(const MatvecParams& p, int nseg, int parts, int cus, int (&count)[kMaxSegments]) {
   double bytes[kMaxSegments] = {0.0}, total = 0.0;
   for (int j = 0; j < nseg; ++j) {
-    bytes[j] = static_cast<double>(p.seg[j].rows) * S * type_bytes(p.seg[j].type) * parts;
+    bytes[j] = static_cast<double>(p.seg[j].rows) * p.S * type_bytes(p.seg[j].type) * parts;
     total += bytes[j];
   }
-  if (nseg > cus) return hipSuccess;
-  int count[kMaxSegments] = {0}, sum = 0;
+  if (nseg > cus) return false;
+  int sum = 0;
   for (int j = 0; j < nseg; ++j) {
     const int want = static_cast<int>(cus * bytes[j] / total + 0.5);
     count[j] = std::clamp(want, 1, p.seg[j].rows);
@@ -108,6 +99,86 @@ hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t str
     --count[big];
     --sum;
   }
+  return true;
+}
+
+// M = 2..8 (gemv_stream_mt.hpp): MT = 4 or 8 rows, every wave a run of whole
+// rows; needs all MT * K / 8 activation tasks staged (4 per thread) and one
+// weight type in all segments.
+hipError_t launch_stream_mt(const MatvecParams& p, int mode, hipStream_t stream, bool& launched) {
+  int cus = 0, max_lds = 0;
+  hipError_t e = device_limits(cus, max_lds);
+  if (e != hipSuccess) return e;
+  const int MT = p.M <= 4 ? 4 : 8;
+  if (MT * (p.K / 8) > 64 * kStreamWaves * kMtXStaged) return hipSuccess;
+  const int nseg = mode == 1 ? 1 : p.nseg;
+  const int parts = mode == 1 ? 2 : 1, wpp = kStreamWaves / parts;
+  const int64_t S = p.S;
+  for (int j = 1; j < nseg; ++j)
+    if (p.seg[j].type != p.seg[0].type) return hipSuccess;  // one weight type per launch
+  int count[kMaxSegments] = {0};
+  if (!workgroup_counts(p, nseg, parts, cus, count)) return hipSuccess;
+
+  StreamMtParams sp{};
+  sp.x = p.x;
+  sp.h = p.h;
+  sp.M = p.M;
+  sp.K = p.K;
+  sp.S = p.S;
+  sp.nseg = nseg;
+  int64_t region = 16, sums = 0;
+  int begin = 0;
+  for (int j = 0; j < nseg; ++j) {
+    const int per = p.seg[j].rows / count[j], rem = p.seg[j].rows % count[j];
+    const int64_t rb = S * type_bytes(p.seg[j].type);
+    const int64_t rows_max = per + (rem ? 1 : 0);
+    const int64_t rpw = (rows_max + wpp - 1) / wpp;
+    region = std::max<int64_t>(region, (2 + rpw * rb + 15) / 16 * 16);
+    for (int64_t n : {static_cast<int64_t>(per), rows_max}) {  // the workgroups' row counts
+      if (n == 0) continue;
+      const int64_t groups = (n + 15) / 16;
+      const int64_t ranges = std::min<int64_t>(S, std::max<int64_t>(1, (kStreamWaves + parts * groups - 1) / (parts * groups)));
+      sums = std::max(sums, n * ranges * MT);
+    }
+    sp.seg[j] = {p.seg[j].w, p.seg[j].y, p.seg[j].rows, p.seg[j].type, begin, per, rem, 0};
+    begin += count[j];
+  }
+  if (mode == 1) sp.seg[1] = {p.seg[1].w, nullptr, p.seg[1].rows, p.seg[1].type, 0, 0, 0, 0};
+  const int64_t J = (region + 1023) / 1024;
+  if (J > kStreamMaxJ) return hipSuccess;
+  const int64_t lds = MT * S * 8 * static_cast<int64_t>(sizeof(qk_q8_block)) + kStreamWaves * region +
+                      parts * sums * 4;
+  if (lds > max_lds) return hipSuccess;
+  sp.region = static_cast<int32_t>(region);
+  sp.sums_stride = static_cast<int32_t>(sums);
+  const int type = p.seg[0].type;
+  const StreamMtKernel fn = MT == 4 ? stream_mt_kernel_m4(type, static_cast<int>(J), mode)
+                                    : stream_mt_kernel_m8(type, static_cast<int>(J), mode);
+  if (!fn) return hipSuccess;
+  e = allow_lds(reinterpret_cast<const void*>(fn), static_cast<int>(lds));
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(begin)), dim3(64 * kStreamWaves),
+                     static_cast<size_t>(lds), stream, sp);
+  launched = true;
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t stream, bool& launched) {
+  launched = false;
+  if (p.x == nullptr || (mode != 0 && mode != 1) || p.M > 8) return hipSuccess;
+  if (p.M > 1) return launch_stream_mt(p, mode, stream, launched);
+  if (p.K > kStreamMaxK) return hipSuccess;
+  int cus = 0, max_lds = 0;
+  hipError_t e = device_limits(cus, max_lds);
+  if (e != hipSuccess) return e;
+  const int nseg = mode == 1 ? 1 : p.nseg;
+  const int parts = mode == 1 ? 2 : 1, wpp = kStreamWaves / parts;
+  const int64_t S = p.S;
+
+  int count[kMaxSegments] = {0};
+  if (!workgroup_counts(p, nseg, parts, cus, count)) return hipSuccess;
 
   StreamParams sp{};
   sp.x = p.x;
@@ -139,7 +210,7 @@ hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t str
   if (lds > max_lds) return hipSuccess;
   const StreamKernel fn = stream_kernel(type, J, mode);
   if (!fn) return hipSuccess;
-  e = allow_lds(fn, static_cast<int>(lds));
+  e = allow_lds(reinterpret_cast<const void*>(fn), static_cast<int>(lds));
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(begin)), dim3(64 * kStreamWaves),
                      static_cast<size_t>(lds), stream, sp);

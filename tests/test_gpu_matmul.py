@@ -262,7 +262,9 @@ def test_matmul_generic_widths(gpu, oracle, qtype, K):
 
 @pytest.mark.parametrize("qtype", [Q4, Q6])
 def test_matmul_entry_points_agree_bitwise(gpu, oracle, qtype):
-    """qk_matmul, qk_matmul_ws and qk_quantize_q8 + qk_matmul_q8 give identical bits."""
+    """qk_matmul and qk_matmul_ws give identical bits; qk_quantize_q8 + qk_matmul_q8
+    (the streaming kernel, pre-quantised input) the same integer dots added in
+    another order."""
     K, N, M = 2560, 1000, 2
     w = make_weight(gpu, oracle, qtype, N, K, SEED + 9)
     x = oracle.synth_normal(M * K, SEED + 10)
@@ -279,7 +281,8 @@ def test_matmul_entry_points_agree_bitwise(gpu, oracle, qtype):
     gpu.matmul_q8(q8, w, qtype, K, N, y, M)
     gpu.synchronize()
     c = y.download(np.float32).reshape(M, N)
-    assert np.array_equal(a, b) and np.array_equal(a, c)
+    assert np.array_equal(a, b)
+    assert oracle.row_norm_error(c, a.astype(np.float64)) <= 1e-6
 
 
 @pytest.mark.parametrize("M", [1, 3, 8, 11])

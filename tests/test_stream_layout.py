@@ -130,3 +130,140 @@ def test_whole_share_indices_in_bounds(rows, types, K, mode):
 
 def test_lm_head_takes_the_streaming_kernel():
     assert launcher([151936], [14], 2560, 0) is None
+
+
+# ---- the batched whole-share kernel (gemv_stream_mt.hpp), M = 2..8 ----
+
+MT_XSTAGED = 4
+
+
+def launcher_mt(rows, types, K, mode, M):
+    """(counts, per/rem, J, region, sums_stride, lds, MT) or None (streaming kernel)."""
+    S = K // 256
+    MT = 4 if M <= 4 else 8
+    if MT * (K // 8) > 64 * WAVES * MT_XSTAGED:
+        return None
+    nseg = 1 if mode == 1 else len(rows)
+    parts = 2 if mode == 1 else 1
+    wpp = WAVES // parts
+    if any(types[j] != types[0] for j in range(nseg)):
+        return None  # one weight type per launch
+    byt = [rows[j] * S * BYTES[types[j]] * parts for j in range(nseg)]
+    total = float(sum(byt))
+    count = [min(max(int(CUS * b / total + 0.5), 1), rows[j]) for j, b in enumerate(byt)]
+    while sum(count) > CUS:
+        count[count.index(max(count))] -= 1
+    region, sums = 16, 0
+    for j in range(nseg):
+        per, rem = rows[j] // count[j], rows[j] % count[j]
+        rb = S * BYTES[types[j]]
+        rows_max = per + (1 if rem else 0)
+        rpw = -(-rows_max // wpp)
+        region = max(region, (2 + rpw * rb + 15) // 16 * 16)
+        for n in (per, rows_max):
+            if n == 0:
+                continue
+            groups = -(-n // 16)
+            ranges = min(S, max(1, -(-WAVES // (parts * groups))))
+            sums = max(sums, n * ranges * MT)
+    J = -(-region // 1024)
+    if J > MAX_J:
+        return None
+    lds = MT * S * 8 * 48 + WAVES * region + parts * sums * 4
+    if lds > MAX_LDS:
+        return None
+    return count, J, region, sums, lds, MT
+
+
+def check_shape_mt(rows, types, K, mode, M, bases):
+    cfg = launcher_mt(rows, types, K, mode, M)
+    if cfg is None:
+        return False
+    count, J, region, sums_stride, lds, MT = cfg
+    S = K // 256
+    parts = 2 if mode == 1 else 1
+    wpp = WAVES // parts
+    nseg = 1 if mode == 1 else len(rows)
+    for j in range(nseg):
+        B = BYTES[types[j]]
+        rb = S * B
+        per, rem = rows[j] // count[j], rows[j] % count[j]
+        seen = np.zeros((parts, rows[j]), np.int64)
+        for g in range(count[j]):
+            r0 = g * per + min(g, rem)
+            nrows = per + (1 if g < rem else 0)
+            rpw = -(-nrows // wpp)
+            images = {}
+            for wave in range(WAVES):
+                part, wv = wave // wpp, wave % wpp
+                first = min(wv * rpw, nrows)
+                wrows = min(rpw, nrows - first)
+                base = bases[1] if (mode == 1 and part == 1) else bases[j]
+                run = base + (r0 + (first if wrows > 0 else 0)) * rb
+                o = run & 3
+                run4 = run - o
+                L = max((o + wrows * rb + 15) >> 4, 1)
+                end = base + rows[j] * rb
+                last = base + ((rows[j] * rb + 3) & ~3) - 16
+                c = np.minimum(np.arange(64)[:, None] + 64 * np.arange(J)[None, :], L - 1)
+                a = np.minimum(run4 + 16 * c, last)
+                assert np.all(a >= base) and np.all(a + 16 <= ((end + 3) & ~3)) and np.all(a % 4 == 0)
+                off = a - run4
+                assert np.all(off >= 0) and np.all(off + 16 <= region)
+                cov = np.zeros(region, bool)
+                for x in np.unique(off):
+                    cov[x:x + 16] = True
+                images[wave] = (cov, o, first, wrows)
+                if wrows > 0:
+                    assert cov[o:o + wrows * rb].all()
+                    seen[part, r0 + first: r0 + first + wrows] += 1
+            # compute units: every (part, row, s) piece read lies in its owner's written bytes
+            groups = -(-nrows // 16)
+            ranges = min(S, max(1, -(-WAVES // (parts * groups))))
+            o_base = (bases[j] + r0 * rb) & 3
+            for part in range(parts):
+                for row in range(nrows):
+                    owner = part * wpp + row // rpw
+                    first = (row // rpw) * rpw
+                    o_owner = (o_base + first * (rb & 3)) & 3
+                    cov, o, f2, wrows = images[owner]
+                    assert f2 == first and o == o_owner
+                    rowp = o_owner + (row - first) * rb
+                    assert cov[rowp:rowp + rb].all()
+                    for rr in range(ranges):
+                        assert (row * ranges + rr) * MT + MT - 1 < sums_stride
+            assert nrows * M <= 64 * WAVES * 64  # row-total threads loop
+        assert np.all(seen == 1), "every row of every part exactly once"
+    assert lds <= MAX_LDS
+    return True
+
+
+MT_SHAPES = [
+    ([9728, 9728], [12, 12], 2560, 1, 8),           # gate + up, M = 8
+    ([4096, 1024, 1024], [12, 12, 12], 2560, 0, 8),  # q/k/v all Q4_K, M = 8
+    ([2560], [12], 4096, 0, 8),                      # attn_output, M = 8
+    ([4096, 1024, 1024], [14, 14, 14], 2560, 0, 3),
+    ([5], [14], 2560, 0, 3),
+    ([1000], [12], 2560, 0, 2),
+    ([4096, 4096], [14, 14], 2560, 1, 2),
+    ([101], [14], 1280, 0, 5),
+    ([3, 1, 2], [12, 12, 12], 256, 0, 7),
+]
+
+
+@pytest.mark.parametrize("rows,types,K,mode,M", MT_SHAPES)
+def test_batched_whole_share_indices_in_bounds(rows, types, K, mode, M):
+    bases = [(1 << 24) * (i + 1) + (4 if t == 14 else 0) for i, t in enumerate(types)]
+    assert check_shape_mt(rows, types, K, mode, M, bases)
+
+
+def test_batched_mixed_types_take_the_streaming_kernel():
+    assert launcher_mt([4096, 1024, 1024], [12, 12, 14], 2560, 0, 8) is None  # Q4_K q/k, Q6_K v
+
+
+def test_batched_ffn_down_takes_the_streaming_kernel():
+    assert launcher_mt([2560], [14], 9728, 0, 8) is None  # 8 x 9728 activations exceed the staging
+
+
+def test_batched_q6k_gate_up_too_wide_takes_the_streaming_kernel():
+    assert launcher_mt([9728, 9728], [14, 14], 2560, 1, 2) is None  # 5 rows of 2100 B per wave: J > 8
