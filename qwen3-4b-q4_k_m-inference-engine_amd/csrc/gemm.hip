@@ -64,9 +64,12 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
 
 // Q8 round trip of one group of 8 activations (a quad of lanes holds one
 // 32-value block), scaled by `up`, split into fp16 hi/lo at hi + at, lo + at.
+// The quad's first lane also stores 2^-5 * (sum of the block's scaled
+// values) as hi/lo at xs + xs_at (the Q4_K GEMM's min-term operand).
 __device__ __forceinline__ void prep_group(const f32x4 a, const f32x4 b, float up,
                                            _Float16* __restrict__ hi, _Float16* __restrict__ lo,
-                                           int64_t at) {
+                                           int64_t at, _Float16* __restrict__ xs, int64_t xs_at,
+                                           bool first) {
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   float bmax = 0.0f;
 #pragma unroll
@@ -77,14 +80,34 @@ __device__ __forceinline__ void prep_group(const f32x4 a, const f32x4 b, float u
                          0, __builtin_bit_cast(int, bmax), 0x4E, 0xF, 0xF, false)));
   const float scale = bmax / 127.0f;
   uint32_t h[4], l[4];
+  float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float c0 = bmax == 0.0f ? 0.0f : roundf((v[2 * i] / bmax) * 127.0f);
     const float c1 = bmax == 0.0f ? 0.0f : roundf((v[2 * i + 1] / bmax) * 127.0f);
-    split2((c0 * scale) * up, (c1 * scale) * up, h[i], l[i]);
+    const float s0 = (c0 * scale) * up, s1 = (c1 * scale) * up;
+    split2(s0, s1, h[i], l[i]);
+    sum += s0;
+    sum += s1;
   }
   *reinterpret_cast<u32x4*>(hi + at) = u32x4{h[0], h[1], h[2], h[3]};
   *reinterpret_cast<u32x4*>(lo + at) = u32x4{l[0], l[1], l[2], l[3]};
+  sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0xB1,
+                                                               0xF, 0xF, false));
+  sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x4E,
+                                                               0xF, 0xF, false));
+  if (first) {
+    const float t = sum * 0.03125f;
+    const _Float16 th = static_cast<_Float16>(t);
+    xs[xs_at] = th;
+    xs[xs_at + 8] = static_cast<_Float16>(t - static_cast<float>(th));
+  }
+}
+
+// Sub-block sums layout: 32 bytes per (row, superblock of 256 values): the
+// 8 hi halves, then the 8 lo halves. Index (in halves) of block jb's hi value.
+__device__ __forceinline__ int64_t xsum_index(int64_t row, int jb, int S) {
+  return (row * S + (jb >> 3)) * 16 + (jb & 7);
 }
 
 constexpr int kPrepGroups = 8;  // groups of 8 activations held per thread: K <= 16384 in one pass
@@ -96,7 +119,8 @@ constexpr int kPrepGroups = 8;  // groups of 8 activations held per thread: K <=
 __global__ __launch_bounds__(256) void prep_rows_kernel(const float* __restrict__ x,
                                                         _Float16* __restrict__ hi,
                                                         _Float16* __restrict__ lo,
-                                                        float* __restrict__ row_scale, int K) {
+                                                        float* __restrict__ row_scale,
+                                                        _Float16* __restrict__ xs, int K) {
   __shared__ float partial[4];
   const int64_t row = blockIdx.x;
   const float* xr = x + row * K;
@@ -136,12 +160,15 @@ __global__ __launch_bounds__(256) void prep_rows_kernel(const float* __restrict_
 #pragma unroll
     for (int i = 0; i < kPrepGroups; ++i) {
       const int g = tid + 256 * i;
-      if (g < groups) prep_group(va[i], vb[i], up, hi, lo, row * K + 8 * g);
+      if (g < groups)
+        prep_group(va[i], vb[i], up, hi, lo, row * K + 8 * g, xs, xsum_index(row, g >> 2, K / 256),
+                   (g & 3) == 0);
     }
   } else {
     for (int g = tid; g < groups; g += 256)
       prep_group(*reinterpret_cast<const f32x4_a4*>(xr + 8 * g),
-                 *reinterpret_cast<const f32x4_a4*>(xr + 8 * g + 4), up, hi, lo, row * K + 8 * g);
+                 *reinterpret_cast<const f32x4_a4*>(xr + 8 * g + 4), up, hi, lo, row * K + 8 * g,
+                 xs, xsum_index(row, g >> 2, K / 256), (g & 3) == 0);
   }
 }
 
@@ -480,21 +507,30 @@ hipError_t launch_gemm_type(const GemmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Workspace: hi [M x K] and lo [M x K] fp16 planes, row scales [M] fp32, then
+// (16-byte aligned) the sub-block sums, 32 bytes per (row, 256 values).
 struct WorkspaceLayout {
   _Float16* hi;
   _Float16* lo;
   float* row_scale;
+  _Float16* xs;
 };
+
+size_t xsum_offset(int64_t M, int64_t K) {
+  const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(K) * 4 + static_cast<size_t>(M) * 4;
+  return (bytes + 15) & ~size_t{15};
+}
 
 WorkspaceLayout layout(void* workspace, int64_t M, int64_t K) {
   auto* base = static_cast<_Float16*>(workspace);
-  return {base, base + M * K, reinterpret_cast<float*>(base + 2 * M * K)};
+  return {base, base + M * K, reinterpret_cast<float*>(base + 2 * M * K),
+          reinterpret_cast<_Float16*>(static_cast<char*>(workspace) + xsum_offset(M, K))};
 }
 
 }  // namespace
 
 size_t gemm_workspace_bytes(int64_t M, int64_t K) {
-  const size_t bytes = static_cast<size_t>(M) * static_cast<size_t>(K) * 4 + static_cast<size_t>(M) * 4;
+  const size_t bytes = xsum_offset(M, K) + static_cast<size_t>(M) * static_cast<size_t>(K / 256) * 32;
   return (bytes + 255) & ~size_t{255};
 }
 
@@ -502,13 +538,15 @@ hipError_t launch_gemm_prep(const float* x, int64_t M, int64_t K, void* workspac
                             hipStream_t stream) {
   const WorkspaceLayout ws = layout(workspace, M, K);
   prep_rows_kernel<<<static_cast<uint32_t>(M), 256, 0, stream>>>(x, ws.hi, ws.lo, ws.row_scale,
-                                                                  static_cast<int>(K));
+                                                                  ws.xs, static_cast<int>(K));
   return hipGetLastError();
 }
 
 hipError_t launch_gemm_core(const void* workspace, const void* w, int type, int64_t K, int64_t N,
                             float* y, int64_t M, hipStream_t stream) {
   const WorkspaceLayout ws = layout(const_cast<void*>(workspace), M, K);
+  if (type == QK_TYPE_Q4_K && gemm_q4k_fits(M, K, N))
+    return launch_gemm_q4k(ws.hi, ws.row_scale, ws.xs, w, K, N, y, M, stream);
   const GemmArgs a{ws.hi, ws.lo, ws.row_scale, static_cast<const uint8_t*>(w), y,
                    static_cast<int>(M), static_cast<int>(N), static_cast<int>(K)};
   return type == QK_TYPE_Q4_K ? launch_gemm_type<QK_TYPE_Q4_K>(a, stream)

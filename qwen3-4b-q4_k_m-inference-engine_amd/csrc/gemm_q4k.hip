@@ -1,0 +1,349 @@
+// Q4_K dequantize-GEMM for prefill (M > 8 activation rows) on MFMA, with
+// integer-structured weight operands.
+//
+// Replaces project<Q4_K> launched with gridDim.y = rows (src/cuda/matmul.cu:151-158).
+// With w = d*sc_j*q - dmin*m_j (src/cuda/embedding.cu:6-32) and x8 the Q8 round
+// trip of x (MatmulReference.hpp:11-29), each superblock of a weight row adds
+//     d * sum_k v[m,k] * (sc_j*q)[n,k]  -  32*dmin * sum_j m_j * X[m,j]
+// to 2^s(m) * y[m,n], where (gemm.hip, prep_rows_kernel)
+//   v = 2^s x8, held as fp16 planes hi + lo (22 significant bits),
+//   X[m,j] = 2^-5 * (sum of v over sub-block j), also as hi + lo.
+// sc_j*q <= 63*15 is an exact fp16 integer, so every 16-deep MFMA step is
+// hi*B + lo*B with one unsplit weight operand and no per-block scaling; d
+// and dmin fold in once per superblock and the min term is one more MFMA per
+// superblock (A = X hi in k 0-7 and X lo in k 8-15, B = m_j in both halves).
+//
+// Workgroup: 4 waves side by side in N, each owning TM x TN tiles of 32 x 32
+// of the (BM = 32 TM) x (BN = 128 TN) output tile. K runs in stages of 64
+// weights (one 32-byte qs group: sub-blocks 2g, 2g+1 of a superblock):
+//   - the activation tile of a stage (BM rows x hi/lo x 64 halves) goes
+//     through one of two LDS slots: the workgroup loads stage c+3 into
+//     registers while it computes stage c and writes stage c+1 (loaded two
+//     stages earlier) after it; one barrier per stage;
+//   - each lane loads its own weight bytes (the superblock header and its
+//     16 qs bytes of each stage: one 128-byte line per row) into registers
+//     a superblock ahead, and its sub-block sums once per superblock: no
+//     weight tile in LDS.
+// Rows past M or N are clamped to the last row on load and not stored.
+//
+// MFMA operand rule (v_mfma_f32_32x32x16_f16, checked on the device): lane l
+// gives row l%32 of A and column l%32 of B with the same 8 k values, half-wave
+// l/32 choosing which 8; D lane l, register r holds row 8*(r/4) + 4*(l/32) +
+// r%4, column l%32. The k order inside a step is free as long as A and B
+// agree: in step (u, s) of a stage, half-wave h takes the 8 weights at
+// qs bytes 16h + 8s .. +7 of the group, nibble u (sub-block 2g + u), i.e.
+// stage-local k = 32u + 16h + 8s + e. An A slot row is 256 bytes: the 8
+// hi and 8 lo 16-byte pieces, piece L = 8*plane + p stored at position
+// L ^ (row & 15), so the 16 rows a ds_read_b128 serves at once hit 16
+// different bank groups.
+#include "qk_device.hpp"
+#include "qk_launch.hpp"
+
+namespace qk {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) uint8_t lds_byte;
+typedef __attribute__((address_space(3))) half8 lds_half8;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4_t;
+
+constexpr int kWaves = 4;
+constexpr int kStageK = 64;  // weights of K per stage
+
+template <int TM, int TN>
+struct Q4KCfg {
+  static constexpr int BM = 32 * TM;
+  static constexpr int BN = 32 * TN * kWaves;
+  static constexpr int SLOT = BM * 2 * 2 * kStageK;         // BM rows of hi + lo, 64 halves each
+  static constexpr int PIECES = SLOT / 16 / (64 * kWaves);  // 16-byte A pieces per thread
+  static_assert(PIECES >= 1 && SLOT % (16 * 64 * kWaves) == 0, "whole pieces per thread");
+};
+
+struct Q4KGemmArgs {
+  const _Float16* hi;  // [M x K]; lo follows at + M*K
+  const _Float16* xs;  // sub-block sums: [M][S][hi 8, lo 8]
+  const float* row_scale;
+  const uint8_t* w;
+  float* y;
+  int32_t M, N, K, S;
+  int32_t n_tiles, tiles, per_xcd, pad;
+};
+
+// 8 weights (bytes of dwords lo, hi; nibble U) -> fp16 sc*q.
+// (1024 + q) is the fp16 with bits 0x6400 | q; one fused multiply-add
+// (1024 + q)*sc - 1024*sc gives sc*q exactly (U = 1 holds 16q in the byte:
+// (1024 + 16q)*(sc/16) - 64*sc).
+template <int U>
+__device__ __forceinline__ half8 weights_fp16(uint32_t lo, uint32_t hi, half2v c, half2v e) {
+  constexpr uint32_t mask = U ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+  const uint32_t a = lo & mask, b = hi & mask;
+  auto pair = [&](uint32_t v, uint32_t sel) {
+    const half2v h = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, v, sel));
+    return __builtin_elementwise_fma(h, c, e);
+  };
+  const half2v p0 = pair(a, 0x04010400u), p1 = pair(a, 0x04030402u);
+  const half2v p2 = pair(b, 0x04010400u), p3 = pair(b, 0x04030402u);
+  return half8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+template <int TM, int TN>
+__global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmArgs args) {
+  using C = Q4KCfg<TM, TN>;
+  __shared__ __align__(16) uint8_t slots[2][C::SLOT];
+  const int b = static_cast<int>(blockIdx.x);
+  // Consecutive tiles go to one XCD (workgroups are dealt to the 8 XCDs in
+  // turn) and run along N first, so an XCD keeps one activation tile in its
+  // L2 while the weight tiles stream past it.
+  const int t = (b & 7) * args.per_xcd + (b >> 3);
+  if ((b >> 3) >= args.per_xcd || t >= args.tiles) return;
+  const int mt = t / args.n_tiles, nt = t % args.n_tiles;
+  const int m0 = mt * C::BM, n0 = nt * C::BN;
+  const int M = args.M, N = args.N, K = args.K, S = args.S;
+  const int nst = 4 * S;
+
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+
+  // Activation pieces of this thread: f = tid + 256 v -> row f / 16,
+  // position f % 16 holding piece L = (f % 16) ^ (row & 15) (plane L / 8,
+  // 8 halves at 8 (L % 8)); LDS byte 16 f.
+  const _Float16* pa[C::PIECES];
+#pragma unroll
+  for (int v = 0; v < C::PIECES; ++v) {
+    const int f = tid + 64 * kWaves * v;
+    const int row = f >> 4, piece = (f & 15) ^ (row & 15);
+    pa[v] = args.hi + (piece >> 3 ? static_cast<int64_t>(M) * K : 0) +
+            static_cast<int64_t>(min(m0 + row, M - 1)) * K + 8 * (piece & 7);
+  }
+  // Weight rows of this lane (one per n-tile) and sub-block sum rows (one per m-tile).
+  const uint8_t* wrow[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+    wrow[j] = args.w +
+              static_cast<int64_t>(min(n0 + wave * 32 * TN + 32 * j + l32, N - 1)) * S * kQ4KBytes;
+  const _Float16* xrow[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+    xrow[i] = args.xs + static_cast<int64_t>(min(m0 + 32 * i + l32, M - 1)) * S * 16 + 8 * h;
+
+  auto load_a = [&](int c, u32x4 (&r)[C::PIECES]) {
+#pragma unroll
+    for (int v = 0; v < C::PIECES; ++v) r[v] = load16(pa[v] + kStageK * c);
+  };
+  auto store_a = [&](int slot, const u32x4 (&r)[C::PIECES]) {
+#pragma unroll
+    for (int v = 0; v < C::PIECES; ++v)
+      *reinterpret_cast<lds_u32x4_t*>((lds_byte*)slots[slot] + 16 * (tid + 64 * kWaves * v)) = r[v];
+  };
+  // A superblock's weight bytes of this lane: the header and, per stage g,
+  // qs bytes 32g + 16h .. +15 (one 128-byte line per row, read at once).
+  auto load_w = [&](int sb, u32x4 (&hd)[TN], u32x4 (&q)[TN][4]) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const uint8_t* p = wrow[j] + sb * kQ4KBytes;
+      hd[j] = load16(p);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) q[j][g] = load16(p + 16 + 32 * g + 16 * h);
+    }
+  };
+  auto load_x = [&](int sb, u32x4 (&x)[TM]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) x[i] = load16(xrow[i] + 16 * sb);
+  };
+
+  // acc: the output tile; ph / pl: this superblock's hi and lo products
+  // (separate accumulators: independent MFMA chains)
+  f32x16 acc[TM][TN], ph[TM][TN], pl[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = ph[i][j][r] = pl[i][j][r] = 0.0f;
+
+  // In flight across stages: areg[p] (activations of the stages of parity
+  // p, loaded three stages ahead of their use), wh / wq [p] (weight bytes of
+  // the superblocks of parity p, loaded during the superblock before) and xa
+  // (this superblock's sub-block sums). Every loaded dword is used, so no
+  // load destination is recycled early, and the superblock loop is unrolled
+  // by two so no loaded register is copied at the loop edge.
+  u32x4 areg[2][C::PIECES], wh[2][TN], wq[2][TN][4], xa[TM];
+  load_a(0, areg[0]);
+  load_w(0, wh[0], wq[0]);
+  load_x(0, xa);
+  store_a(0, areg[0]);
+  load_a(min(1, nst - 1), areg[1]);
+  load_a(min(2, nst - 1), areg[0]);
+  __syncthreads();
+
+  const int swz = l32 & 15;  // row & 15 of every A row this lane reads
+  auto superblock = [&](int sb, const u32x4 (&hcur)[TN], const u32x4 (&qcur)[TN][4],
+                        u32x4 (&hnext)[TN], u32x4 (&qnext)[TN][4]) {
+    u32x4 min_b[TN];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c = 4 * sb + g;
+      __builtin_amdgcn_sched_barrier(0);  // nothing of stage c+1 moves above stage c's work
+
+      // weight-side constants of sub-blocks 2g (nibble 0) and 2g+1 (nibble 1)
+      half2v cm[TN][2], ce[TN][2];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const u32x4 hd = hcur[j];
+        int sc0, mn0, sc1, mn1;
+        scale_min_k4(2 * g, hd.y, hd.z, hd.w, sc0, mn0);
+        scale_min_k4(2 * g + 1, hd.y, hd.z, hd.w, sc1, mn1);
+        const _Float16 s0 = static_cast<_Float16>(static_cast<uint16_t>(sc0));
+        const _Float16 s1 = static_cast<_Float16>(static_cast<uint16_t>(sc1));
+        cm[j][0] = half2v{s0, s0};
+        ce[j][0] = cm[j][0] * half2v{-1024.0f16, -1024.0f16};
+        const half2v t1{s1, s1};
+        cm[j][1] = t1 * half2v{0.0625f16, 0.0625f16};
+        ce[j][1] = t1 * half2v{-64.0f16, -64.0f16};
+        const half2v mm{static_cast<_Float16>(static_cast<uint16_t>(mn0)),
+                        static_cast<_Float16>(static_cast<uint16_t>(mn1))};
+        min_b[j][g] = __builtin_bit_cast(uint32_t, mm);
+      }
+
+      // A fragments are read one step ahead of their MFMAs
+      const lds_byte* a_row = (const lds_byte*)slots[g & 1] + l32 * 256;
+      auto read_a = [&](int step, half8 (&ah)[TM], half8 (&al)[TM]) {
+        const int p = 4 * (step >> 1) + 2 * h + (step & 1);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          ah[i] = *reinterpret_cast<const lds_half8*>(a_row + 32 * i * 256 + 16 * (p ^ swz));
+          al[i] = *reinterpret_cast<const lds_half8*>(a_row + 32 * i * 256 + 16 * ((8 + p) ^ swz));
+        }
+      };
+      half8 ah[2][TM], al[2][TM];
+      read_a(0, ah[0], al[0]);
+#pragma unroll
+      for (int step = 0; step < 4; ++step) {
+        const int U = step >> 1, s = step & 1;
+        if (step < 3) read_a(step + 1, ah[(step + 1) & 1], al[(step + 1) & 1]);
+        half8 bw[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const u32x4 q = qcur[j][g];
+          bw[j] = U ? weights_fp16<1>(q[2 * s], q[2 * s + 1], cm[j][1], ce[j][1])
+                    : weights_fp16<0>(q[2 * s], q[2 * s + 1], cm[j][0], ce[j][0]);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[step & 1][i], bw[j], ph[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            pl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[step & 1][i], bw[j], pl[i][j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+
+      // stage c+1's activations (loaded two stages ago) into the other
+      // slot, then start loading stage c+3 into the same registers
+      store_a((g + 1) & 1, areg[(g + 1) & 1]);
+      load_a(min(c + 3, nst - 1), areg[(g + 1) & 1]);
+      // the next superblock's weight bytes, issued after this stage's
+      // activation loads (vector loads complete in order: the next two
+      // stages' waits for activations do not wait for these)
+      if (g == 2) load_w(min(sb + 1, S - 1), hnext, qnext);
+
+      if (g == 3) {  // superblock end: acc += d * part - 32 dmin * (X . m)
+        float dd[TN], dm[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          dd[j] = half_bits_to_float(hcur[j].x & 0xFFFFu);
+          dm[j] = -32.0f * half_bits_to_float(hcur[j].x >> 16);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(dd[j], ph[i][j][r] + pl[i][j][r], acc[i][j][r]);
+            f32x16 zero;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
+            ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                __builtin_bit_cast(half8, xa[i]), __builtin_bit_cast(half8, min_b[j]), zero, 0, 0, 0);
+          }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              acc[i][j][r] = fmaf(dm[j], ph[i][j][r], acc[i][j][r]);
+              ph[i][j][r] = 0.0f;
+              pl[i][j][r] = 0.0f;
+            }
+        load_x(min(sb + 1, S - 1), xa);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+    }
+  };
+  for (int sb = 0; sb < S; sb += 2) {
+    superblock(sb, wh[0], wq[0], wh[1], wq[1]);
+    if (sb + 1 < S) superblock(sb + 1, wh[1], wq[1], wh[0], wq[0]);
+  }
+
+  // epilogue: y = acc * 2^-s(m)
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (m >= M) continue;
+      const float rs = args.row_scale[m];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + wave * 32 * TN + 32 * j + l32;
+        if (n < N) args.y[static_cast<int64_t>(m) * N + n] = acc[i][j][r] * rs;
+      }
+    }
+}
+
+template <int TM, int TN>
+hipError_t launch_cfg(Q4KGemmArgs a, hipStream_t stream) {
+  using C = Q4KCfg<TM, TN>;
+  a.n_tiles = (a.N + C::BN - 1) / C::BN;
+  a.tiles = a.n_tiles * ((a.M + C::BM - 1) / C::BM);
+  a.per_xcd = (a.tiles + 7) / 8;
+  hipLaunchKernelGGL((gemm_q4k_kernel<TM, TN>), dim3(static_cast<uint32_t>(8 * a.per_xcd)),
+                     dim3(64 * kWaves), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_q4k_fits(int64_t M, int64_t K, int64_t N) {
+  return K % 256 == 0 && M > 0 && N > 0 && M <= (1 << 30) && N <= (1 << 30);
+}
+
+hipError_t launch_gemm_q4k(const _Float16* hi, const float* row_scale, const void* xsums,
+                           const void* w, int64_t K, int64_t N, float* y, int64_t M,
+                           hipStream_t stream) {
+  Q4KGemmArgs a{};
+  a.hi = hi;
+  a.xs = static_cast<const _Float16*>(xsums);
+  a.row_scale = row_scale;
+  a.w = static_cast<const uint8_t*>(w);
+  a.y = y;
+  a.M = static_cast<int32_t>(M);
+  a.N = static_cast<int32_t>(N);
+  a.K = static_cast<int32_t>(K);
+  a.S = static_cast<int32_t>(K / 256);
+#ifndef QK_Q4K_CFG
+#define QK_Q4K_CFG 2, 1
+#endif
+  return launch_cfg<QK_Q4K_CFG>(a, stream);
+}
+
+}  // namespace qk
