@@ -78,14 +78,17 @@ int qk_version(void);
  * allocated. M > 8 (prefill): the activations' Q8 round trip, scaled per row
  * by a power of two, is stored as two fp16 planes hi + lo in a stream-ordered
  * scratch buffer (qk_matmul_workspace_size bytes, allocated and freed on
- * `stream` like the reference's per-call workspace); an MFMA GEMM runs on
- * weights dequantised in LDS and split the same way, summing hi*hi + hi*lo +
- * lo*hi in fp32 (operands carry 22 significant bits). */
+ * `stream` like the reference's per-call workspace) with the planes' 32-value
+ * block sums; an MFMA GEMM multiplies them by the weights in fp32 accumulation:
+ * Q4_K as the exact fp16 integers sc*q (hi*B + lo*B per step, d and dmin*m
+ * applied once per superblock), Q6_K dequantised in LDS and split into hi + lo
+ * (hi*hi + hi*lo + lo*hi). */
 int qk_matmul(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
               int64_t M, qk_stream_t stream);
 
 /* Workspace bytes qk_matmul_ws needs for this shape: 0 for M <= 8, else
- * M*K*4 + M*4 rounded up to 256 (0 for shapes qk_matmul rejects). */
+ * M*K*4 + M*4 rounded up to 16, plus M*(K/256)*32, rounded up to 256 (0 for
+ * shapes qk_matmul rejects). */
 size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M);
 
 /* qk_matmul with a caller-owned device workspace (16-byte aligned) of at least

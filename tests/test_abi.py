@@ -82,8 +82,9 @@ def test_other_validation(qk):
     assert lib.qk_quantize_q8(None, 1, 100, None, None) == 1
     assert lib.qk_matmul_workspace_size(12, 2560, 8, 3) == 0  # Q8 runs inside the kernel
     # M > 8: two fp16 planes (hi, lo) of M x K plus M row scales, rounded up to 256
-    assert lib.qk_matmul_workspace_size(12, 2560, 8, 9) == 92416  # 9*2560*4 + 36 -> 361*256
-    assert lib.qk_matmul_workspace_size(14, 256, 8, 11) == 11520  # 11*256*4 + 44 -> 45*256
+    # 9*2560*4 + 36 (hi/lo planes, row scales) -> 92208, + 9*10*32 sub-block sums -> 372*256
+    assert lib.qk_matmul_workspace_size(12, 2560, 8, 9) == 95232
+    assert lib.qk_matmul_workspace_size(14, 256, 8, 11) == 11776  # 11*256*4 + 44 -> 11312, + 11*32 -> 46*256
     assert lib.qk_matmul_workspace_size(14, 2500, 8, 11) == 0  # rejected shape
     p = ctypes.c_void_p(256)
     assert lib.qk_matmul_ws(p, p, 12, 2560, 8, p, 9, None, 0, None) == 1  # M > 8 needs scratch
