@@ -17,13 +17,12 @@
 // of the (BM = 32 TM) x (BN = 128 TN) output tile. K runs in stages of 64
 // weights (one 32-byte qs group: sub-blocks 2g, 2g+1 of a superblock):
 //   - the activation tile of a stage (BM rows x hi/lo x 64 halves) goes
-//     through one of two LDS slots: the workgroup loads stage c+3 into
-//     registers while it computes stage c and writes stage c+1 (loaded two
-//     stages earlier) after it; one barrier per stage;
-//   - each lane loads its own weight bytes (the superblock header and its
-//     16 qs bytes of each stage: one 128-byte line per row) into registers
-//     a superblock ahead, and its sub-block sums once per superblock: no
-//     weight tile in LDS.
+//     through one of two LDS slots: the workgroup loads stage c+2 into
+//     registers while it computes stage c and writes stage c+1 (loaded a
+//     stage earlier) in the middle of it; one barrier per stage;
+//   - each lane loads its own weight bytes into registers (its 16 qs bytes
+//     a stage ahead, the superblock header during the superblock before)
+//     and its sub-block sums once per superblock: no weight tile in LDS.
 // Rows past M or N are clamped to the last row on load and not stored.
 //
 // MFMA operand rule (v_mfma_f32_32x32x16_f16, checked on the device): lane l
@@ -36,6 +35,9 @@
 // hi and 8 lo 16-byte pieces, piece L = 8*plane + p stored at position
 // L ^ (row & 15), so the 16 rows a ds_read_b128 serves at once hit 16
 // different bank groups.
+#include <map>
+#include <mutex>
+
 #include "qk_device.hpp"
 #include "qk_launch.hpp"
 
@@ -139,16 +141,15 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
     for (int v = 0; v < C::PIECES; ++v)
       *reinterpret_cast<lds_u32x4_t*>((lds_byte*)slots[slot] + 16 * (tid + 64 * kWaves * v)) = r[v];
   };
-  // A superblock's weight bytes of this lane: the header and, per stage g,
-  // qs bytes 32g + 16h .. +15 (one 128-byte line per row, read at once).
-  auto load_w = [&](int sb, u32x4 (&hd)[TN], u32x4 (&q)[TN][4]) {
+  // This lane's weight bytes: a superblock's header, and the qs bytes
+  // 32g + 16h .. +15 of stage c = 4 sb + g.
+  auto load_head = [&](int sb, u32x4 (&hd)[TN]) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const uint8_t* p = wrow[j] + sb * kQ4KBytes;
-      hd[j] = load16(p);
+    for (int j = 0; j < TN; ++j) hd[j] = load16(wrow[j] + sb * kQ4KBytes);
+  };
+  auto load_q = [&](int c, u32x4 (&q)[TN]) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) q[j][g] = load16(p + 16 + 32 * g + 16 * h);
-    }
+    for (int j = 0; j < TN; ++j) q[j] = load16(wrow[j] + (c >> 2) * kQ4KBytes + 16 + 32 * (c & 3) + 16 * h);
   };
   auto load_x = [&](int sb, u32x4 (&x)[TM]) {
 #pragma unroll
@@ -165,28 +166,29 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = ph[i][j][r] = pl[i][j][r] = 0.0f;
 
-  // In flight across stages: areg[p] (activations of the stages of parity
-  // p, loaded three stages ahead of their use), wh / wq [p] (weight bytes of
-  // the superblocks of parity p, loaded during the superblock before) and xa
-  // (this superblock's sub-block sums). Every loaded dword is used, so no
-  // load destination is recycled early, and the superblock loop is unrolled
-  // by two so no loaded register is copied at the loop edge.
-  u32x4 areg[2][C::PIECES], wh[2][TN], wq[2][TN][4], xa[TM];
-  load_a(0, areg[0]);
-  load_w(0, wh[0], wq[0]);
+  // In flight across stages: areg (activations, loaded in stage c-1 and
+  // stored to LDS in stage c for stage c+1), bq[p] (qs bytes of the stages of
+  // parity p, loaded a stage ahead), wh[p] (headers of the superblocks of
+  // parity p, loaded during the superblock before) and xa (this superblock's
+  // sub-block sums). Every loaded dword is used, so no load destination is
+  // recycled early, and the superblock loop is unrolled by two so no loaded
+  // register is copied at the loop edge.
+  u32x4 areg[C::PIECES], wh[2][TN], bq[2][TN], xa[TM];
+  load_a(0, areg);
+  load_head(0, wh[0]);
+  load_q(0, bq[0]);
   load_x(0, xa);
-  store_a(0, areg[0]);
-  load_a(min(1, nst - 1), areg[1]);
-  load_a(min(2, nst - 1), areg[0]);
+  store_a(0, areg);
+  load_a(min(1, nst - 1), areg);
   __syncthreads();
 
   const int swz = l32 & 15;  // row & 15 of every A row this lane reads
-  auto superblock = [&](int sb, const u32x4 (&hcur)[TN], const u32x4 (&qcur)[TN][4],
-                        u32x4 (&hnext)[TN], u32x4 (&qnext)[TN][4]) {
+  auto superblock = [&](int sb, const u32x4 (&hcur)[TN], u32x4 (&hnext)[TN]) {
     u32x4 min_b[TN];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int c = 4 * sb + g;
+      load_q(min(c + 1, nst - 1), bq[(g + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);  // nothing of stage c+1 moves above stage c's work
 
       // weight-side constants of sub-blocks 2g (nibble 0) and 2g+1 (nibble 1)
@@ -209,7 +211,10 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
         min_b[j][g] = __builtin_bit_cast(uint32_t, mm);
       }
 
-      // A fragments are read one step ahead of their MFMAs
+      // Steps: the MFMAs of step s interleaved with the weight conversion of
+      // step s+1 and the A fragment reads of step s+2 (two fragment buffers);
+      // the stage's activation staging (store of stage c+1, loads of stage
+      // c+3) sits between steps 1 and 2, under their MFMAs.
       const lds_byte* a_row = (const lds_byte*)slots[g & 1] + l32 * 256;
       auto read_a = [&](int step, half8 (&ah)[TM], half8 (&al)[TM]) {
         const int p = 4 * (step >> 1) + 2 * h + (step & 1);
@@ -219,40 +224,51 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
           al[i] = *reinterpret_cast<const lds_half8*>(a_row + 32 * i * 256 + 16 * ((8 + p) ^ swz));
         }
       };
-      half8 ah[2][TM], al[2][TM];
-      read_a(0, ah[0], al[0]);
-#pragma unroll
-      for (int step = 0; step < 4; ++step) {
+      auto convert = [&](int step, half8 (&bw)[TN]) {
         const int U = step >> 1, s = step & 1;
-        if (step < 3) read_a(step + 1, ah[(step + 1) & 1], al[(step + 1) & 1]);
-        half8 bw[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const u32x4 q = qcur[j][g];
+          const u32x4 q = bq[g & 1][j];
           bw[j] = U ? weights_fp16<1>(q[2 * s], q[2 * s + 1], cm[j][1], ce[j][1])
                     : weights_fp16<0>(q[2 * s], q[2 * s + 1], cm[j][0], ce[j][0]);
         }
+      };
+      half8 ah[2][TM], al[2][TM], bw[2][TN];
+      read_a(0, ah[0], al[0]);
+      read_a(1, ah[1], al[1]);
+      convert(0, bw[0]);
+#pragma unroll
+      for (int step = 0; step < 4; ++step) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
-            ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[step & 1][i], bw[j], ph[i][j], 0, 0, 0);
+          for (int j = 0; j < TN; ++j) {
+            ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[step & 1][i], bw[step & 1][j], ph[i][j], 0, 0, 0);
+            pl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[step & 1][i], bw[step & 1][j], pl[i][j], 0, 0, 0);
+          }
+        if (step < 3) convert(step + 1, bw[(step + 1) & 1]);
+        if (step < 2) read_a(step + 2, ah[step & 1], al[step & 1]);
+        if (step == 1) {
+          // stage c+1's activations (loaded a stage ago) into the other
+          // slot, then start loading stage c+2 into the same registers
+          store_a((g + 1) & 1, areg);
+          load_a(min(c + 2, nst - 1), areg);
+          // the next superblock's headers, issued after this stage's
+          // activation loads (vector loads complete in order: the next
+          // stage's wait for activations does not wait for these)
+          if (g == 2) load_head(min(sb + 1, S - 1), hnext);
+        }
+        // one MFMA, then a share of the VALU and LDS work, repeated
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            pl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[step & 1][i], bw[j], pl[i][j], 0, 0, 0);
+        for (int k = 0; k < 2 * TM * TN; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
-
-      // stage c+1's activations (loaded two stages ago) into the other
-      // slot, then start loading stage c+3 into the same registers
-      store_a((g + 1) & 1, areg[(g + 1) & 1]);
-      load_a(min(c + 3, nst - 1), areg[(g + 1) & 1]);
-      // the next superblock's weight bytes, issued after this stage's
-      // activation loads (vector loads complete in order: the next two
-      // stages' waits for activations do not wait for these)
-      if (g == 2) load_w(min(sb + 1, S - 1), hnext, qnext);
 
       if (g == 3) {  // superblock end: acc += d * part - 32 dmin * (X . m)
         float dd[TN], dm[TN];
@@ -290,8 +306,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
     }
   };
   for (int sb = 0; sb < S; sb += 2) {
-    superblock(sb, wh[0], wq[0], wh[1], wq[1]);
-    if (sb + 1 < S) superblock(sb + 1, wh[1], wq[1], wh[0], wq[0]);
+    superblock(sb, wh[0], wh[1]);
+    if (sb + 1 < S) superblock(sb + 1, wh[1], wh[0]);
   }
 
   // epilogue: y = acc * 2^-s(m)
@@ -308,6 +324,25 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
         if (n < N) args.y[static_cast<int64_t>(m) * N + n] = acc[i][j][r] * rs;
       }
     }
+}
+
+// Compute units of the current device (queried once per device).
+hipError_t compute_units(int& cus) {
+  static std::mutex mutex;
+  static std::map<int, int> known;
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mutex);
+  auto it = known.find(device);
+  if (it == known.end()) {
+    int c = 0;
+    e = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return e;
+    it = known.emplace(device, c).first;
+  }
+  cus = it->second;
+  return hipSuccess;
 }
 
 template <int TM, int TN>
@@ -340,10 +375,12 @@ hipError_t launch_gemm_q4k(const _Float16* hi, const float* row_scale, const voi
   a.N = static_cast<int32_t>(N);
   a.K = static_cast<int32_t>(K);
   a.S = static_cast<int32_t>(K / 256);
-#ifndef QK_Q4K_CFG
-#define QK_Q4K_CFG 2, 1
-#endif
-  return launch_cfg<QK_Q4K_CFG>(a, stream);
+  // 64 x 128 tiles when they give every CU at least two workgroups, else
+  // 32 x 128 (twice the workgroups, each half the rows)
+  int cus = 256;
+  if (hipError_t e = compute_units(cus); e != hipSuccess) return e;
+  const int64_t tiles64 = ((M + 63) / 64) * ((N + 127) / 128);
+  return tiles64 >= 2 * cus ? launch_cfg<2, 1>(a, stream) : launch_cfg<1, 1>(a, stream);
 }
 
 }  // namespace qk

@@ -166,7 +166,7 @@ def run_model(cfg, oracle, M, N, K, seed):
     return y, np.asarray(ref, np.float64).reshape(M, N)
 
 
-@pytest.mark.parametrize("TM,TN", [(2, 1), (1, 2)])
+@pytest.mark.parametrize("TM,TN", [(2, 1), (1, 1)])  # the two tiles the launcher uses
 def test_q4k_gemm_model_matches_oracle(oracle, TM, TN):
     y, ref = run_model(Cfg(TM, TN), oracle, M=70, N=300, K=512, seed=91)
     err = oracle.row_norm_error(y, ref)

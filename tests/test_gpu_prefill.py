@@ -117,10 +117,12 @@ def test_prefill_activation_scale_invariance(gpu, oracle, qtype, scale):
 
 @pytest.mark.parametrize("qtype", [Q4, Q6])
 @pytest.mark.parametrize("M,N,K", [(9, 77, 2560), (100, 1000, 512), (129, 64, 256),
-                                   (300, 130, 768), (257, 3, 3328), (16, 64, 16640)])
+                                   (300, 130, 768), (257, 3, 3328), (16, 64, 16640),
+                                   (200, 20000, 512)])
 def test_prefill_ragged_against_oracle(gpu, oracle, qtype, M, N, K):
-    """Row and column counts off the 128 x 64 tiling, narrow and odd widths
-    (K = 16640 takes the activation prep's two-pass path), against the
+    """Row and column counts off the tilings (Q4_K: 32 x 128 and, for grids
+    of 512+ tiles like 200 x 20000, 64 x 128; Q6_K: 128 x 64), narrow and odd
+    widths (K = 16640 takes the activation prep's two-pass path), against the
     oracle's own double-accumulated product."""
     print(f"[case] type={qtype} M={M} N={N} K={K}", flush=True)
     w = make_weight(gpu, qtype, N, K, SEED + 20 + M + N)
