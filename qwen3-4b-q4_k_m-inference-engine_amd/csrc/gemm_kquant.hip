@@ -1,7 +1,18 @@
-// Q4_K dequantize-GEMM for prefill (M > 8 activation rows) on MFMA, with
-// integer-structured weight operands.
+// Q4_K / Q6_K dequantize-GEMM for prefill (M > 8 activation rows) on MFMA,
+// with integer-structured weight operands.
 //
-// Replaces project<Q4_K> launched with gridDim.y = rows (src/cuda/matmul.cu:151-158).
+// Replaces project<Q4_K/Q6_K> launched with gridDim.y = rows
+// (src/cuda/matmul.cu:151-158).
+//
+// Q6_K (w = d*sc*q, q in -32..31, sc int8; src/cuda/embedding.cu:34-59): the
+// weight operand is sc*q, |sc*q| <= 4096, held as B_hi = fp16(sc*q) and the
+// exact remainder B_lo = sc*q - B_hi in {-1, 0, 1} (fp16 integers are exact
+// to 2048, even numbers to 4096), so a step is hi*B_hi + lo*B_hi + hi*B_lo
+// and d folds in once per superblock; no min term. A stage is 64 weights of
+// one half (128 weights) of the superblock: groups a and a+2 (a = stage & 1),
+// which share the qh bytes; a lane takes l = 16h .. 16h+15 of both.
+//
+// Q4_K:
 // With w = d*sc_j*q - dmin*m_j (src/cuda/embedding.cu:6-32) and x8 the Q8 round
 // trip of x (MatmulReference.hpp:11-29), each superblock of a weight row adds
 //     d * sum_k v[m,k] * (sc_j*q)[n,k]  -  32*dmin * sum_j m_j * X[m,j]
@@ -55,7 +66,7 @@ constexpr int kWaves = 4;
 constexpr int kStageK = 64;  // weights of K per stage
 
 template <int TM, int TN>
-struct Q4KCfg {
+struct KQCfg {
   static constexpr int BM = 32 * TM;
   static constexpr int BN = 32 * TN * kWaves;
   static constexpr int SLOT = BM * 2 * 2 * kStageK;         // BM rows of hi + lo, 64 halves each
@@ -63,9 +74,9 @@ struct Q4KCfg {
   static_assert(PIECES >= 1 && SLOT % (16 * 64 * kWaves) == 0, "whole pieces per thread");
 };
 
-struct Q4KGemmArgs {
+struct KQGemmArgs {
   const _Float16* hi;  // [M x K]; lo follows at + M*K
-  const _Float16* xs;  // sub-block sums: [M][S][hi 8, lo 8]
+  const _Float16* xs;  // sub-block sums: [M][S][hi 8, lo 8] (Q4_K only)
   const float* row_scale;
   const uint8_t* w;
   float* y;
@@ -90,9 +101,39 @@ __device__ __forceinline__ half8 weights_fp16(uint32_t lo, uint32_t hi, half2v c
   return half8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-template <int TM, int TN>
-__global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmArgs args) {
-  using C = Q4KCfg<TM, TN>;
+// 8 Q6_K weights (ql bytes of dwords l0/l1, nibble U; qh bytes of h0/h1,
+// bits shift..shift+1) -> fp16 sc*q as hi + exact lo. Each byte's 6-bit code
+// c becomes the fp16 1024 + c (bits 0x6400 | c); minus 1056 gives q exactly;
+// q*sc rounds once to hi and fma(q, sc, -hi) is the exact remainder.
+template <int U>
+__device__ __forceinline__ void weights_q6k(uint32_t l0, uint32_t l1, uint32_t h0, uint32_t h1,
+                                            uint32_t shift, half2v sc, half8& bh, half8& bl) {
+  auto code = [shift](uint32_t l, uint32_t hb) {
+    return ((U ? l >> 4 : l) & 0x0F0F0F0Fu) | (((hb >> shift) & 0x03030303u) << 4);
+  };
+  const uint32_t c0 = code(l0, h0), c1 = code(l1, h1);
+  half2v q[4];
+  const uint32_t sel[2] = {0x04010400u, 0x04030402u};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    q[i] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, i < 2 ? c0 : c1, sel[i & 1])) +
+           half2v{-1056.0f16, -1056.0f16};
+  half2v hi[4], lo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hi[i] = q[i] * sc;
+    lo[i] = __builtin_elementwise_fma(q[i], sc, -hi[i]);
+  }
+  bh = half8{hi[0].x, hi[0].y, hi[1].x, hi[1].y, hi[2].x, hi[2].y, hi[3].x, hi[3].y};
+  bl = half8{lo[0].x, lo[0].y, lo[1].x, lo[1].y, lo[2].x, lo[2].y, lo[3].x, lo[3].y};
+}
+
+template <int TYPE, int TM, int TN>
+__global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArgs args) {
+  using C = KQCfg<TM, TN>;
+  constexpr bool kQ6 = TYPE == QK_TYPE_Q6_K;
+  constexpr int B = kQ6 ? kQ6KBytes : kQ4KBytes;  // superblock bytes
+  constexpr int QW = kQ6 ? 2 : 1;                 // 16-byte weight loads per stage and n-tile
   __shared__ __align__(16) uint8_t slots[2][C::SLOT];
   const int b = static_cast<int>(blockIdx.x);
   // Consecutive tiles go to one XCD (workgroups are dealt to the 8 XCDs in
@@ -111,22 +152,28 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
   const int h = lane >> 5, l32 = lane & 31;
 
   // Activation pieces of this thread: f = tid + 256 v -> row f / 16,
-  // position f % 16 holding piece L = (f % 16) ^ (row & 15) (plane L / 8,
-  // 8 halves at 8 (L % 8)); LDS byte 16 f.
+  // position f % 16 holding piece L = (f % 16) ^ (row & 15) of plane L / 8;
+  // piece p = L % 8 of a stage is its 8 halves at stage-local k 8p (Q4_K:
+  // the stage is k 64c .. 64c+63) or 64 (p / 4) + 8 (p % 4) (Q6_K: groups
+  // a and a+2 of a superblock half); LDS byte 16 f.
   const _Float16* pa[C::PIECES];
 #pragma unroll
   for (int v = 0; v < C::PIECES; ++v) {
     const int f = tid + 64 * kWaves * v;
-    const int row = f >> 4, piece = (f & 15) ^ (row & 15);
+    const int row = f >> 4, piece = (f & 15) ^ (row & 15), p = piece & 7;
     pa[v] = args.hi + (piece >> 3 ? static_cast<int64_t>(M) * K : 0) +
-            static_cast<int64_t>(min(m0 + row, M - 1)) * K + 8 * (piece & 7);
+            static_cast<int64_t>(min(m0 + row, M - 1)) * K + (kQ6 ? 64 * (p >> 2) + 8 * (p & 3) : 8 * p);
   }
+  // first halves of stage c: Q4_K 64c; Q6_K 256 sb + 128 (half) + 32 a
+  auto stage_k = [](int c) {
+    return kQ6 ? 256 * (c >> 2) + 128 * ((c >> 1) & 1) + 32 * (c & 1) : kStageK * c;
+  };
   // Weight rows of this lane (one per n-tile) and sub-block sum rows (one per m-tile).
   const uint8_t* wrow[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j)
     wrow[j] = args.w +
-              static_cast<int64_t>(min(n0 + wave * 32 * TN + 32 * j + l32, N - 1)) * S * kQ4KBytes;
+              static_cast<int64_t>(min(n0 + wave * 32 * TN + 32 * j + l32, N - 1)) * S * B;
   const _Float16* xrow[TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -134,22 +181,42 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
 
   auto load_a = [&](int c, u32x4 (&r)[C::PIECES]) {
 #pragma unroll
-    for (int v = 0; v < C::PIECES; ++v) r[v] = load16(pa[v] + kStageK * c);
+    for (int v = 0; v < C::PIECES; ++v) r[v] = load16(pa[v] + stage_k(c));
   };
   auto store_a = [&](int slot, const u32x4 (&r)[C::PIECES]) {
 #pragma unroll
     for (int v = 0; v < C::PIECES; ++v)
       *reinterpret_cast<lds_u32x4_t*>((lds_byte*)slots[slot] + 16 * (tid + 64 * kWaves * v)) = r[v];
   };
-  // This lane's weight bytes: a superblock's header, and the qs bytes
-  // 32g + 16h .. +15 of stage c = 4 sb + g.
-  auto load_head = [&](int sb, u32x4 (&hd)[TN]) {
+  // This lane's weight bytes. Per superblock: Q4_K its header (d, dmin, 12
+  // scale bytes); Q6_K its 16 scales and d (superblocks are 2-byte aligned).
+  // Per stage c = 4 sb + g: Q4_K qs bytes 32g + 16h .. +15; Q6_K ql bytes
+  // 64 (g/2) + 32 (g%2) + 16h .. +15 and qh bytes 32 (g/2) + 16h .. +15.
+  auto load_head = [&](int sb, u32x4 (&hd)[TN], uint32_t (&dd)[TN]) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) hd[j] = load16(wrow[j] + sb * kQ4KBytes);
+    for (int j = 0; j < TN; ++j) {
+      const uint8_t* p = wrow[j] + sb * B;
+      if constexpr (kQ6) {
+        hd[j] = load16_a2(p + 192);
+        dd[j] = load_u16(p + 208);
+      } else {
+        hd[j] = load16(p);
+        dd[j] = 0;
+      }
+    }
   };
-  auto load_q = [&](int c, u32x4 (&q)[TN]) {
+  auto load_q = [&](int c, u32x4 (&q)[TN][QW]) {
+    const int g = c & 3;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) q[j] = load16(wrow[j] + (c >> 2) * kQ4KBytes + 16 + 32 * (c & 3) + 16 * h);
+    for (int j = 0; j < TN; ++j) {
+      const uint8_t* p = wrow[j] + (c >> 2) * B;
+      if constexpr (kQ6) {
+        q[j][0] = load16_a2(p + 64 * (g >> 1) + 32 * (g & 1) + 16 * h);
+        q[j][1] = load16_a2(p + 128 + 32 * (g >> 1) + 16 * h);
+      } else {
+        q[j][0] = load16(p + 16 + 32 * g + 16 * h);
+      }
+    }
   };
   auto load_x = [&](int sb, u32x4 (&x)[TM]) {
 #pragma unroll
@@ -173,17 +240,19 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
   // sub-block sums). Every loaded dword is used, so no load destination is
   // recycled early, and the superblock loop is unrolled by two so no loaded
   // register is copied at the loop edge.
-  u32x4 areg[C::PIECES], wh[2][TN], bq[2][TN], xa[TM];
+  u32x4 areg[C::PIECES], wh[2][TN], bq[2][TN][QW], xa[TM];
+  uint32_t wd[2][TN];
   load_a(0, areg);
-  load_head(0, wh[0]);
+  load_head(0, wh[0], wd[0]);
   load_q(0, bq[0]);
-  load_x(0, xa);
+  if constexpr (!kQ6) load_x(0, xa);
   store_a(0, areg);
   load_a(min(1, nst - 1), areg);
   __syncthreads();
 
   const int swz = l32 & 15;  // row & 15 of every A row this lane reads
-  auto superblock = [&](int sb, const u32x4 (&hcur)[TN], u32x4 (&hnext)[TN]) {
+  auto superblock = [&](int sb, const u32x4 (&hcur)[TN], const uint32_t (&dcur)[TN],
+                        u32x4 (&hnext)[TN], uint32_t (&dnext)[TN]) {
     u32x4 min_b[TN];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -191,11 +260,23 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
       load_q(min(c + 1, nst - 1), bq[(g + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);  // nothing of stage c+1 moves above stage c's work
 
-      // weight-side constants of sub-blocks 2g (nibble 0) and 2g+1 (nibble 1)
+      // weight-side constants. Q4_K: of sub-blocks 2g (nibble 0) and 2g+1
+      // (nibble 1); Q6_K: the scales of groups a and a+2 for this lane's l
+      // (index 8 (g/2) + 2 (a + 2U) + h: byte 2a + h of dword 2 (g/2) + U)
       half2v cm[TN][2], ce[TN][2];
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const u32x4 hd = hcur[j];
+        if constexpr (kQ6) {
+#pragma unroll
+          for (int U = 0; U < 2; ++U) {
+            const int sc = __builtin_amdgcn_sbfe(static_cast<int>(hd[2 * (g >> 1) + U]),
+                                                 8 * (2 * (g & 1)) + 8 * h, 8);
+            const _Float16 sh = static_cast<_Float16>(static_cast<int16_t>(sc));
+            cm[j][U] = half2v{sh, sh};
+          }
+          continue;
+        }
         int sc0, mn0, sc1, mn1;
         scale_min_k4(2 * g, hd.y, hd.z, hd.w, sc0, mn0);
         scale_min_k4(2 * g + 1, hd.y, hd.z, hd.w, sc1, mn1);
@@ -224,19 +305,28 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
           al[i] = *reinterpret_cast<const lds_half8*>(a_row + 32 * i * 256 + 16 * ((8 + p) ^ swz));
         }
       };
-      auto convert = [&](int step, half8 (&bw)[TN]) {
+      // bw: the weight operand (Q6_K: bw = hi, bx = exact remainder)
+      auto convert = [&](int step, half8 (&bw)[TN], half8 (&bx)[TN]) {
         const int U = step >> 1, s = step & 1;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const u32x4 q = bq[g & 1][j];
-          bw[j] = U ? weights_fp16<1>(q[2 * s], q[2 * s + 1], cm[j][1], ce[j][1])
-                    : weights_fp16<0>(q[2 * s], q[2 * s + 1], cm[j][0], ce[j][0]);
+          const u32x4 q = bq[g & 1][j][0];
+          if constexpr (kQ6) {
+            const u32x4 qh = bq[g & 1][j][QW - 1];
+            if (U)
+              weights_q6k<1>(q[2 * s], q[2 * s + 1], qh[2 * s], qh[2 * s + 1], 2 * (g & 1) + 4, cm[j][1], bw[j], bx[j]);
+            else
+              weights_q6k<0>(q[2 * s], q[2 * s + 1], qh[2 * s], qh[2 * s + 1], 2 * (g & 1), cm[j][0], bw[j], bx[j]);
+          } else {
+            bw[j] = U ? weights_fp16<1>(q[2 * s], q[2 * s + 1], cm[j][1], ce[j][1])
+                      : weights_fp16<0>(q[2 * s], q[2 * s + 1], cm[j][0], ce[j][0]);
+          }
         }
       };
-      half8 ah[2][TM], al[2][TM], bw[2][TN];
+      half8 ah[2][TM], al[2][TM], bw[2][TN], bx[2][TN];
       read_a(0, ah[0], al[0]);
       read_a(1, ah[1], al[1]);
-      convert(0, bw[0]);
+      convert(0, bw[0], bx[0]);
 #pragma unroll
       for (int step = 0; step < 4; ++step) {
 #pragma unroll
@@ -245,8 +335,10 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
           for (int j = 0; j < TN; ++j) {
             ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[step & 1][i], bw[step & 1][j], ph[i][j], 0, 0, 0);
             pl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[step & 1][i], bw[step & 1][j], pl[i][j], 0, 0, 0);
+            if constexpr (kQ6)
+              ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[step & 1][i], bx[step & 1][j], ph[i][j], 0, 0, 0);
           }
-        if (step < 3) convert(step + 1, bw[(step + 1) & 1]);
+        if (step < 3) convert(step + 1, bw[(step + 1) & 1], bx[(step + 1) & 1]);
         if (step < 2) read_a(step + 2, ah[step & 1], al[step & 1]);
         if (step == 1) {
           // stage c+1's activations (loaded a stage ago) into the other
@@ -256,13 +348,13 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
           // the next superblock's headers, issued after this stage's
           // activation loads (vector loads complete in order: the next
           // stage's wait for activations does not wait for these)
-          if (g == 2) load_head(min(sb + 1, S - 1), hnext);
+          if (g == 2) load_head(min(sb + 1, S - 1), hnext, dnext);
         }
         // one MFMA, then a share of the VALU and LDS work, repeated
 #pragma unroll
-        for (int k = 0; k < 2 * TM * TN; ++k) {
+        for (int k = 0; k < (kQ6 ? 3 : 2) * TM * TN; ++k) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, kQ6 ? 5 : 3, 0);
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
@@ -270,7 +362,21 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
         __builtin_amdgcn_sched_barrier(0);
       }
 
-      if (g == 3) {  // superblock end: acc += d * part - 32 dmin * (X . m)
+      if (kQ6 && g == 3) {  // superblock end: acc += d * part
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const float d = half_bits_to_float(dcur[j]);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              acc[i][j][r] = fmaf(d, ph[i][j][r] + pl[i][j][r], acc[i][j][r]);
+              ph[i][j][r] = 0.0f;
+              pl[i][j][r] = 0.0f;
+            }
+          }
+      }
+      if (!kQ6 && g == 3) {  // superblock end: acc += d * part - 32 dmin * (X . m)
         float dd[TN], dm[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
@@ -306,8 +412,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_q4k_kernel(const Q4KGemmA
     }
   };
   for (int sb = 0; sb < S; sb += 2) {
-    superblock(sb, wh[0], wh[1]);
-    if (sb + 1 < S) superblock(sb + 1, wh[1], wh[0]);
+    superblock(sb, wh[0], wd[0], wh[1], wd[1]);
+    if (sb + 1 < S) superblock(sb + 1, wh[1], wd[1], wh[0], wd[0]);
   }
 
   // epilogue: y = acc * 2^-s(m)
@@ -345,27 +451,27 @@ hipError_t compute_units(int& cus) {
   return hipSuccess;
 }
 
-template <int TM, int TN>
-hipError_t launch_cfg(Q4KGemmArgs a, hipStream_t stream) {
-  using C = Q4KCfg<TM, TN>;
+template <int TYPE, int TM, int TN>
+hipError_t launch_cfg(KQGemmArgs a, hipStream_t stream) {
+  using C = KQCfg<TM, TN>;
   a.n_tiles = (a.N + C::BN - 1) / C::BN;
   a.tiles = a.n_tiles * ((a.M + C::BM - 1) / C::BM);
   a.per_xcd = (a.tiles + 7) / 8;
-  hipLaunchKernelGGL((gemm_q4k_kernel<TM, TN>), dim3(static_cast<uint32_t>(8 * a.per_xcd)),
+  hipLaunchKernelGGL((gemm_kq_kernel<TYPE, TM, TN>), dim3(static_cast<uint32_t>(8 * a.per_xcd)),
                      dim3(64 * kWaves), 0, stream, a);
   return hipGetLastError();
 }
 
 }  // namespace
 
-bool gemm_q4k_fits(int64_t M, int64_t K, int64_t N) {
+bool gemm_kq_fits(int64_t M, int64_t K, int64_t N) {
   return K % 256 == 0 && M > 0 && N > 0 && M <= (1 << 30) && N <= (1 << 30);
 }
 
-hipError_t launch_gemm_q4k(const _Float16* hi, const float* row_scale, const void* xsums,
-                           const void* w, int64_t K, int64_t N, float* y, int64_t M,
-                           hipStream_t stream) {
-  Q4KGemmArgs a{};
+hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, const void* xsums,
+                          const void* w, int64_t K, int64_t N, float* y, int64_t M,
+                          hipStream_t stream) {
+  KQGemmArgs a{};
   a.hi = hi;
   a.xs = static_cast<const _Float16*>(xsums);
   a.row_scale = row_scale;
@@ -375,12 +481,20 @@ hipError_t launch_gemm_q4k(const _Float16* hi, const float* row_scale, const voi
   a.N = static_cast<int32_t>(N);
   a.K = static_cast<int32_t>(K);
   a.S = static_cast<int32_t>(K / 256);
-  // 64 x 128 tiles when they give every CU at least two workgroups, else
-  // 32 x 128 (twice the workgroups, each half the rows)
+  // 64 x 128 tiles when the grid is large enough, else 32 x 128 (twice the
+  // workgroups, each half the rows). Measured at M = 512 on MI355X: Q4_K
+  // takes 64 x 128 from two tiles per CU (ffn_gate) and 32 x 128 below
+  // (attn_q/k, attn_output); Q6_K, whose stages cost more, takes 64 x 128
+  // from half a tile per CU (ffn_down: 141 us against 189) and 32 x 128 below
+  // (attn_v).
   int cus = 256;
   if (hipError_t e = compute_units(cus); e != hipSuccess) return e;
   const int64_t tiles64 = ((M + 63) / 64) * ((N + 127) / 128);
-  return tiles64 >= 2 * cus ? launch_cfg<2, 1>(a, stream) : launch_cfg<1, 1>(a, stream);
+  if (type == QK_TYPE_Q6_K)
+    return 2 * tiles64 >= cus ? launch_cfg<QK_TYPE_Q6_K, 2, 1>(a, stream)
+                              : launch_cfg<QK_TYPE_Q6_K, 1, 1>(a, stream);
+  return tiles64 >= 2 * cus ? launch_cfg<QK_TYPE_Q4_K, 2, 1>(a, stream)
+                            : launch_cfg<QK_TYPE_Q4_K, 1, 1>(a, stream);
 }
 
 }  // namespace qk

@@ -68,13 +68,13 @@ hipError_t launch_gemm_prep(const float* x, int64_t M, int64_t K, void* workspac
 hipError_t launch_gemm_core(const void* workspace, const void* w, int type, int64_t K, int64_t N,
                             float* y, int64_t M, hipStream_t stream);
 
-// The Q4_K GEMM (gemm_q4k.hip) over the prepared planes: hi (lo follows it),
-// row scales and sub-block sums of the workspace. gemm_q4k_fits: its 32-bit
-// buffer offsets cover the activations and the weights.
-bool gemm_q4k_fits(int64_t M, int64_t K, int64_t N);
-hipError_t launch_gemm_q4k(const _Float16* hi, const float* row_scale, const void* xsums,
-                           const void* w, int64_t K, int64_t N, float* y, int64_t M,
-                           hipStream_t stream);
+// The Q4_K / Q6_K GEMM (gemm_kquant.hip) over the prepared planes: hi (lo
+// follows it), row scales and (Q4_K) sub-block sums of the workspace.
+// gemm_kq_fits: the shape is within its 32-bit tile and row indices.
+bool gemm_kq_fits(int64_t M, int64_t K, int64_t N);
+hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, const void* xsums,
+                          const void* w, int64_t K, int64_t N, float* y, int64_t M,
+                          hipStream_t stream);
 
 // Bytes of the argmax workspace (zero-filled once by the caller).
 size_t argmax_workspace_bytes();

@@ -1,5 +1,5 @@
-"""CPU model of the Q4_K prefill GEMM (qwen3-4b-q4_k_m-inference-engine_amd/
-csrc/gemm_q4k.hip) and of the prep kernel's sub-block sums (csrc/gemm.hip):
+"""CPU model of the Q4_K / Q6_K prefill GEMM (qwen3-4b-q4_k_m-inference-engine_amd/
+csrc/gemm_kquant.hip) and of the prep kernel's sub-block sums (csrc/gemm.hip):
 every load address (activation pieces, weight qs bytes and headers, sub-block
 sums, rows clamped into the matrices), the LDS slot image the workgroup
 writes, every lane's fragment reads from it, the k order shared by the A and
@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 WAVES, STAGE_K = 4, 64
-Q4K_BYTES = 144
+BYTES = {12: 144, 14: 210}
 
 
 class Cfg:
@@ -66,10 +66,22 @@ def scale_min_k4(j, sc12):
     return (sc12[j + 4] & 15) | ((sc12[j - 4] >> 6) << 4), (sc12[j + 4] >> 4) | ((sc12[j] >> 6) << 4)
 
 
-def run_model(cfg, oracle, M, N, K, seed):
+def stage_k(q6, c):
+    """First half of stage c in a row: Q4_K 64c; Q6_K 256 sb + 128 (half) + 32 a."""
+    return 256 * (c >> 2) + 128 * ((c >> 1) & 1) + 32 * (c & 1) if q6 else STAGE_K * c
+
+
+def run_model(cfg, oracle, qtype, M, N, K, seed):
     S, nst = K // 256, K // STAGE_K
+    q6 = qtype == 14
+    SB = BYTES[qtype]
     x = oracle.synth_normal(M * K, seed)
-    w = oracle.synth_superblocks(12, N, K, seed + 1, 0.01, 0.01)
+    if q6:  # scales over the whole int8 range, so sc*q reaches past 2048
+        w = oracle.synth_superblocks(14, N, K, seed + 1, 0.005)
+        sbv = w.reshape(N * S, SB)
+        sbv[:, 192:208] = np.random.default_rng(seed).integers(0, 256, (N * S, 16), dtype=np.uint8)
+    else:
+        w = oracle.synth_superblocks(12, N, K, seed + 1, 0.01, 0.01)
     hi, lo, scale, xs = prep(oracle, x, M, K)
     planes = np.concatenate([hi.reshape(-1), lo.reshape(-1)])  # halves, lo at M*K
     n_tiles = -(-N // cfg.BN)
@@ -88,7 +100,9 @@ def run_model(cfg, oracle, M, N, K, seed):
         for v in range(cfg.PIECES):
             f = tid + 64 * WAVES * v
             row, piece = f >> 4, (f & 15) ^ ((f >> 4) & 15)
-            pa.append(np.where(piece >> 3 == 1, M * K, 0) + np.minimum(m0 + row, M - 1) * K + 8 * (piece & 7))
+            p8 = piece & 7
+            koff = 64 * (p8 >> 2) + 8 * (p8 & 3) if q6 else 8 * p8
+            pa.append(np.where(piece >> 3 == 1, M * K, 0) + np.minimum(m0 + row, M - 1) * K + koff)
         acc = np.zeros((WAVES, cfg.TM, cfg.TN, 32, 32))
         ph = np.zeros_like(acc)
         for sb in range(S):
@@ -97,7 +111,7 @@ def run_model(cfg, oracle, M, N, K, seed):
                 c = 4 * sb + g
                 slot = np.zeros(cfg.SLOT, np.uint8)
                 for v in range(cfg.PIECES):
-                    a = pa[v] + STAGE_K * c
+                    a = pa[v] + stage_k(q6, c)
                     assert np.all(a >= 0) and np.all(a + 8 <= planes.size)
                     f = tid + 64 * WAVES * v
                     assert np.all(16 * f + 16 <= cfg.SLOT)
@@ -106,12 +120,33 @@ def run_model(cfg, oracle, M, N, K, seed):
                 for wv in range(WAVES):
                     n_rows = np.minimum(n0 + wv * 32 * cfg.TN + 32 * np.arange(cfg.TN)[:, None] + l32, N - 1)
                     for j in range(cfg.TN):
-                        base = n_rows[j] * S * Q4K_BYTES + sb * Q4K_BYTES
-                        assert np.all(base + Q4K_BYTES <= w.size)
-                        qoff = base + 16 + 32 * g + 16 * h
-                        assert np.all(qoff + 16 <= base + Q4K_BYTES)
+                        base = n_rows[j] * S * SB + sb * SB
+                        assert np.all(base + SB <= w.size)
                         bw = np.zeros((4, 64, 8))
+                        if q6:
+                            hf, a_ = g >> 1, g & 1
+                            qlo = base + 64 * hf + 32 * a_ + 16 * h
+                            qho = base + 128 + 32 * hf + 16 * h
+                            assert np.all(qlo + 16 <= base + 128) and np.all(qho + 16 <= base + 192)
+                        else:
+                            qoff = base + 16 + 32 * g + 16 * h
+                            assert np.all(qoff + 16 <= base + SB)
                         for L in range(64):
+                            if q6:
+                                ql = w[qlo[L]:qlo[L] + 16].astype(np.int64)
+                                qh = w[qho[L]:qho[L] + 16].astype(np.int64)
+                                scl = w[base[L] + 192:base[L] + 208].view(np.int8).astype(np.int64)
+                                for step in range(4):
+                                    U, s = step >> 1, step & 1
+                                    lo4 = (ql[8 * s:8 * s + 8] >> (4 * U)) & 15
+                                    hi2 = (qh[8 * s:8 * s + 8] >> (2 * a_ + 4 * U)) & 3
+                                    q = (lo4 | (hi2 << 4)) - 32
+                                    sc = scl[8 * hf + 2 * (a_ + 2 * U) + h[L]]
+                                    v = sc * q
+                                    bh = v.astype(np.float16).astype(np.float64)
+                                    assert np.all(np.abs(v - bh) <= 1)  # the exact remainder plane
+                                    bw[step, L] = v
+                                continue
                             head = w[base[L]:base[L] + 16].astype(np.int64)
                             qs = w[qoff[L]:qoff[L] + 16].astype(np.int64)
                             sc0, mn0 = scale_min_k4(2 * g, head[4:16])
@@ -136,11 +171,18 @@ def run_model(cfg, oracle, M, N, K, seed):
             for wv in range(WAVES):
                 n_rows = np.minimum(n0 + wv * 32 * cfg.TN + 32 * np.arange(cfg.TN)[:, None] + l32, N - 1)
                 for i in range(cfg.TM):
+                    if q6:
+                        for j in range(cfg.TN):
+                            base = n_rows[j] * S * SB + sb * SB
+                            d = np.array([np.frombuffer(w[o + 208:o + 210].tobytes(), np.float16)[0] for o in base[:32]], np.float64)
+                            acc[wv, i, j] += d[None, :] * ph[wv, i, j]
+                            ph[wv, i, j] = 0.0
+                        continue
                     xo = np.minimum(m0 + 32 * i + l32, M - 1) * S * 16 + 8 * h + 16 * sb
                     assert np.all(xo + 8 <= xs.size)
                     xa = np.stack([xs[o:o + 8] for o in xo]).astype(np.float64)
                     for j in range(cfg.TN):
-                        base = n_rows[j] * S * Q4K_BYTES + sb * Q4K_BYTES
+                        base = n_rows[j] * S * SB + sb * SB
                         d = np.array([np.frombuffer(w[o:o + 2].tobytes(), np.float16)[0] for o in base[:32]], np.float64)
                         dmin = np.array([np.frombuffer(w[o + 2:o + 4].tobytes(), np.float16)[0] for o in base[:32]], np.float64)
                         mp = np.einsum("hme,hne->mn", xa.reshape(2, 32, 8), min_b[wv, j].reshape(2, 32, 8))
@@ -162,13 +204,14 @@ def run_model(cfg, oracle, M, N, K, seed):
                                 y[m, n] = acc[wv, i, j, mm, nn] * scale[m]
                                 seen[m, n] += 1
     assert np.all(seen == 1), "every output written exactly once"
-    ref = oracle.reference_product(x, w, 12, K, N)
+    ref = oracle.reference_product(x, w, qtype, K, N)
     return y, np.asarray(ref, np.float64).reshape(M, N)
 
 
+@pytest.mark.parametrize("qtype", [12, 14])
 @pytest.mark.parametrize("TM,TN", [(2, 1), (1, 1)])  # the two tiles the launcher uses
-def test_q4k_gemm_model_matches_oracle(oracle, TM, TN):
-    y, ref = run_model(Cfg(TM, TN), oracle, M=70, N=300, K=512, seed=91)
+def test_gemm_model_matches_oracle(oracle, qtype, TM, TN):
+    y, ref = run_model(Cfg(TM, TN), oracle, qtype, M=70, N=300, K=768, seed=91)
     err = oracle.row_norm_error(y, ref)
     print(f"row-norm error {err:.3e}")
     assert err <= 1e-6
