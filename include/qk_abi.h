@@ -81,8 +81,9 @@ int qk_version(void);
  * `stream` like the reference's per-call workspace) with the planes' 32-value
  * block sums; an MFMA GEMM multiplies them by the weights in fp32 accumulation:
  * Q4_K as the exact fp16 integers sc*q (hi*B + lo*B per step, d and dmin*m
- * applied once per superblock), Q6_K dequantised in LDS and split into hi + lo
- * (hi*hi + hi*lo + lo*hi). */
+ * applied once per superblock), Q6_K as sc*q = fp16(sc*q) + an exact
+ * remainder in {-1, 0, 1} (hi*B_hi + lo*B_hi + hi*B_lo, d once per
+ * superblock). Shapes with M or N above 2^30 return QK_ERR_RUNTIME. */
 int qk_matmul(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
               int64_t M, qk_stream_t stream);
 
