@@ -128,7 +128,9 @@ int run_gemm(const float* x, int64_t M, int64_t K, const qk_segment* segments, i
     if (M > (int64_t{1} << 31) - 128 || m_tiles * n_tiles > (int64_t{1} << 31) - 1)
       return fail(QK_ERR_INVALID_ARGUMENT, "matmul rows x columns exceed the launch grid");
   }
-  const size_t need = qk::gemm_workspace_bytes(M, K);
+  size_t need = 0;  // the largest of the segments' needs (they run one after another)
+  for (int j = 0; j < count; ++j)
+    need = std::max(need, qk::gemm_workspace_bytes(M, K, segments[j].type, segments[j].N));
   void* scratch = workspace;
   if (scratch) {
     if (workspace_bytes < need) return fail(QK_ERR_INVALID_ARGUMENT, "matmul workspace too small");
@@ -162,7 +164,7 @@ int qk_version(void) { return 200; }
 
 size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M) {
   if (!supported_type(type) || K <= 0 || K % 256 != 0 || N <= 0 || M <= qk::kGemvMaxRows) return 0;
-  return qk::gemm_workspace_bytes(M, K);
+  return qk::gemm_workspace_bytes(M, K, type, N);
 }
 
 int qk_matmul(const float* x, const void* w, int type, int64_t K, int64_t N, float* y, int64_t M,

@@ -150,7 +150,8 @@ __global__ __launch_bounds__(256) void prep_rows_kernel(const float* __restrict_
 }
 
 // Workspace: hi [M x K] and lo [M x K] fp16 planes, row scales [M] fp32, then
-// (16-byte aligned) the sub-block sums, 32 bytes per (row, 256 values).
+// (16-byte aligned) the sub-block sums, 32 bytes per (row, 256 values), then
+// (256-byte aligned) the GEMM's partial products when it splits K.
 struct WorkspaceLayout {
   _Float16* hi;
   _Float16* lo;
@@ -163,6 +164,11 @@ size_t xsum_offset(int64_t M, int64_t K) {
   return (bytes + 15) & ~size_t{15};
 }
 
+size_t partial_offset(int64_t M, int64_t K) {
+  const size_t bytes = xsum_offset(M, K) + static_cast<size_t>(M) * static_cast<size_t>(K / 256) * 32;
+  return (bytes + 255) & ~size_t{255};
+}
+
 WorkspaceLayout layout(void* workspace, int64_t M, int64_t K) {
   auto* base = static_cast<_Float16*>(workspace);
   return {base, base + M * K, reinterpret_cast<float*>(base + 2 * M * K),
@@ -171,8 +177,8 @@ WorkspaceLayout layout(void* workspace, int64_t M, int64_t K) {
 
 }  // namespace
 
-size_t gemm_workspace_bytes(int64_t M, int64_t K) {
-  const size_t bytes = xsum_offset(M, K) + static_cast<size_t>(M) * static_cast<size_t>(K / 256) * 32;
+size_t gemm_workspace_bytes(int64_t M, int64_t K, int type, int64_t N) {
+  const size_t bytes = partial_offset(M, K) + gemm_kq_partial_bytes(type, M, K, N);
   return (bytes + 255) & ~size_t{255};
 }
 
@@ -188,7 +194,9 @@ hipError_t launch_gemm_core(const void* workspace, const void* w, int type, int6
                             float* y, int64_t M, hipStream_t stream) {
   const WorkspaceLayout ws = layout(const_cast<void*>(workspace), M, K);
   if (!gemm_kq_fits(M, K, N)) return hipErrorInvalidValue;
-  return launch_gemm_kq(type, ws.hi, ws.row_scale, ws.xs, w, K, N, y, M, stream);
+  float* partials = reinterpret_cast<float*>(static_cast<char*>(const_cast<void*>(workspace)) +
+                                             partial_offset(M, K));
+  return launch_gemm_kq(type, ws.hi, ws.row_scale, ws.xs, w, K, N, y, M, partials, stream);
 }
 
 }  // namespace qk

@@ -46,8 +46,7 @@
 // hi and 8 lo 16-byte pieces, piece L = 8*plane + p stored at position
 // L ^ (row & 15), so the 16 rows a ds_read_b128 serves at once hit 16
 // different bank groups.
-#include <map>
-#include <mutex>
+#include <algorithm>
 
 #include "qk_device.hpp"
 #include "qk_launch.hpp"
@@ -81,7 +80,8 @@ struct KQGemmArgs {
   const uint8_t* w;
   float* y;
   int32_t M, N, K, S;
-  int32_t n_tiles, tiles, per_xcd, pad;
+  float* part;  // splits > 1: unscaled partial products [splits][M][N]
+  int32_t n_tiles, tiles, per_xcd, splits;
 };
 
 // 8 weights (bytes of dwords lo, hi; nibble U) -> fp16 sc*q.
@@ -139,12 +139,16 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArg
   // Consecutive tiles go to one XCD (workgroups are dealt to the 8 XCDs in
   // turn) and run along N first, so an XCD keeps one activation tile in its
   // L2 while the weight tiles stream past it.
-  const int t = (b & 7) * args.per_xcd + (b >> 3);
-  if ((b >> 3) >= args.per_xcd || t >= args.tiles) return;
+  // Work unit u = tile * splits + split: split covers superblocks
+  // [sb0, sb1) of K (splits > 1 when the tiles alone leave CUs idle).
+  const int u = (b & 7) * args.per_xcd + (b >> 3);
+  if ((b >> 3) >= args.per_xcd || u >= args.tiles * args.splits) return;
+  const int t = u / args.splits, split = u % args.splits;
   const int mt = t / args.n_tiles, nt = t % args.n_tiles;
   const int m0 = mt * C::BM, n0 = nt * C::BN;
   const int M = args.M, N = args.N, K = args.K, S = args.S;
-  const int nst = 4 * S;
+  const int sb0 = split * S / args.splits, sb1 = (split + 1) * S / args.splits;
+  const int c_last = 4 * sb1 - 1;  // loads past the split's end re-read its last stage
 
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & 63;
@@ -242,12 +246,12 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArg
   // register is copied at the loop edge.
   u32x4 areg[C::PIECES], wh[2][TN], bq[2][TN][QW], xa[TM];
   uint32_t wd[2][TN];
-  load_a(0, areg);
-  load_head(0, wh[0], wd[0]);
-  load_q(0, bq[0]);
-  if constexpr (!kQ6) load_x(0, xa);
+  load_a(4 * sb0, areg);
+  load_head(sb0, wh[0], wd[0]);
+  load_q(4 * sb0, bq[0]);
+  if constexpr (!kQ6) load_x(sb0, xa);
   store_a(0, areg);
-  load_a(min(1, nst - 1), areg);
+  load_a(min(4 * sb0 + 1, c_last), areg);
   __syncthreads();
 
   const int swz = l32 & 15;  // row & 15 of every A row this lane reads
@@ -257,7 +261,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArg
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int c = 4 * sb + g;
-      load_q(min(c + 1, nst - 1), bq[(g + 1) & 1]);
+      load_q(min(c + 1, c_last), bq[(g + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);  // nothing of stage c+1 moves above stage c's work
 
       // weight-side constants. Q4_K: of sub-blocks 2g (nibble 0) and 2g+1
@@ -344,11 +348,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArg
           // stage c+1's activations (loaded a stage ago) into the other
           // slot, then start loading stage c+2 into the same registers
           store_a((g + 1) & 1, areg);
-          load_a(min(c + 2, nst - 1), areg);
+          load_a(min(c + 2, c_last), areg);
           // the next superblock's headers, issued after this stage's
           // activation loads (vector loads complete in order: the next
           // stage's wait for activations does not wait for these)
-          if (g == 2) load_head(min(sb + 1, S - 1), hnext, dnext);
+          if (g == 2) load_head(min(sb + 1, sb1 - 1), hnext, dnext);
         }
         // one MFMA, then a share of the VALU and LDS work, repeated
 #pragma unroll
@@ -405,18 +409,19 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArg
               ph[i][j][r] = 0.0f;
               pl[i][j][r] = 0.0f;
             }
-        load_x(min(sb + 1, S - 1), xa);
+        load_x(min(sb + 1, sb1 - 1), xa);
       }
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
     }
   };
-  for (int sb = 0; sb < S; sb += 2) {
+  for (int sb = sb0; sb < sb1; sb += 2) {
     superblock(sb, wh[0], wd[0], wh[1], wd[1]);
-    if (sb + 1 < S) superblock(sb + 1, wh[1], wd[1], wh[0], wd[0]);
+    if (sb + 1 < sb1) superblock(sb + 1, wh[1], wd[1], wh[0], wd[0]);
   }
 
-  // epilogue: y = acc * 2^-s(m)
+  // epilogue: y = acc * 2^-s(m), or the unscaled partial of this split
+  float* const part = args.part + static_cast<int64_t>(split) * M * N;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -427,28 +432,28 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArg
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int n = n0 + wave * 32 * TN + 32 * j + l32;
-        if (n < N) args.y[static_cast<int64_t>(m) * N + n] = acc[i][j][r] * rs;
+        if (n >= N) continue;
+        if (args.splits == 1)
+          args.y[static_cast<int64_t>(m) * N + n] = acc[i][j][r] * rs;
+        else
+          part[static_cast<int64_t>(m) * N + n] = acc[i][j][r];
       }
     }
 }
 
-// Compute units of the current device (queried once per device).
-hipError_t compute_units(int& cus) {
-  static std::mutex mutex;
-  static std::map<int, int> known;
-  int device = 0;
-  hipError_t e = hipGetDevice(&device);
-  if (e != hipSuccess) return e;
-  std::lock_guard<std::mutex> lock(mutex);
-  auto it = known.find(device);
-  if (it == known.end()) {
-    int c = 0;
-    e = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, device);
-    if (e != hipSuccess) return e;
-    it = known.emplace(device, c).first;
-  }
-  cus = it->second;
-  return hipSuccess;
+// y[m][n] = (partial 0 + partial 1 + ...) * 2^-s(m), the splits added in
+// order (results do not depend on timing). Grid (ceil(N / 256), M).
+__global__ __launch_bounds__(256) void gemm_kq_reduce_kernel(const float* __restrict__ part,
+                                                             const float* __restrict__ row_scale,
+                                                             float* __restrict__ y, int M, int N,
+                                                             int splits) {
+  const int m = static_cast<int>(blockIdx.y);
+  const int n = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (n >= N) return;
+  const int64_t at = static_cast<int64_t>(m) * N + n, plane = static_cast<int64_t>(M) * N;
+  float v = part[at];
+  for (int k = 1; k < splits; ++k) v += part[k * plane + at];
+  y[at] = v * row_scale[m];
 }
 
 template <int TYPE, int TM, int TN>
@@ -456,45 +461,78 @@ hipError_t launch_cfg(KQGemmArgs a, hipStream_t stream) {
   using C = KQCfg<TM, TN>;
   a.n_tiles = (a.N + C::BN - 1) / C::BN;
   a.tiles = a.n_tiles * ((a.M + C::BM - 1) / C::BM);
-  a.per_xcd = (a.tiles + 7) / 8;
+  a.per_xcd = (a.tiles * a.splits + 7) / 8;
   hipLaunchKernelGGL((gemm_kq_kernel<TYPE, TM, TN>), dim3(static_cast<uint32_t>(8 * a.per_xcd)),
                      dim3(64 * kWaves), 0, stream, a);
   return hipGetLastError();
 }
 
+struct KQPlan {
+  bool wide;   // 64 x 128 tiles, else 32 x 128
+  int splits;  // K split into this many superblock ranges
+};
+
+// Tile and split choice, planned for MI355X's 256 CUs (correct on any
+// device): 64 x 128 tiles when the grid is large enough, else 32 x 128
+// (twice the workgroups, each half the rows); measured at M = 512: Q4_K takes
+// 64 x 128 from two tiles per CU (ffn_gate) and 32 x 128 below (attn_q/k,
+// attn_output); Q6_K, whose stages cost more, takes 64 x 128 from half a tile
+// per CU (ffn_down) and 32 x 128 below (attn_v). Grids of fewer than two
+// tiles per CU split a deep K (at most 4 ways, at least 8 superblocks a
+// split) so that about two work units reach every CU; a reduce kernel adds
+// the splits. Measured at M = 512: ffn_down (K = 9728, 3 splits) 102 us
+// with its reduce against 137; at K = 2560 the reduce (~5 us) ate the gain.
+constexpr int64_t kPlanCUs = 256;
+
+KQPlan plan(int type, int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles64 = ((M + 63) / 64) * ((N + 127) / 128);
+  const int64_t tiles32 = ((M + 31) / 32) * ((N + 127) / 128);
+  const bool wide = type == QK_TYPE_Q6_K ? 2 * tiles64 >= kPlanCUs : tiles64 >= 2 * kPlanCUs;
+  const int64_t tiles = wide ? tiles64 : tiles32;
+  const int64_t by_grid = std::clamp<int64_t>(2 * kPlanCUs / tiles, 1, 4);
+  const int64_t by_depth = std::max<int64_t>(K / 256 / 8, 1);
+  return {wide, static_cast<int>(std::min(by_grid, by_depth))};
+}
+
 }  // namespace
 
 bool gemm_kq_fits(int64_t M, int64_t K, int64_t N) {
-  return K % 256 == 0 && M > 0 && N > 0 && M <= (1 << 30) && N <= (1 << 30);
+  return K % 256 == 0 && M > 0 && N > 0 && M <= (1 << 30) && N <= (1 << 30) &&
+         M * N <= (int64_t{1} << 40);
+}
+
+size_t gemm_kq_partial_bytes(int type, int64_t M, int64_t K, int64_t N) {
+  const KQPlan p = plan(type, M, N, K);
+  return p.splits > 1 ? static_cast<size_t>(p.splits) * M * N * sizeof(float) : 0;
 }
 
 hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, const void* xsums,
-                          const void* w, int64_t K, int64_t N, float* y, int64_t M,
+                          const void* w, int64_t K, int64_t N, float* y, int64_t M, float* partials,
                           hipStream_t stream) {
+  const KQPlan p = plan(type, M, N, K);
   KQGemmArgs a{};
   a.hi = hi;
   a.xs = static_cast<const _Float16*>(xsums);
   a.row_scale = row_scale;
   a.w = static_cast<const uint8_t*>(w);
   a.y = y;
+  a.part = partials;
   a.M = static_cast<int32_t>(M);
   a.N = static_cast<int32_t>(N);
   a.K = static_cast<int32_t>(K);
   a.S = static_cast<int32_t>(K / 256);
-  // 64 x 128 tiles when the grid is large enough, else 32 x 128 (twice the
-  // workgroups, each half the rows). Measured at M = 512 on MI355X: Q4_K
-  // takes 64 x 128 from two tiles per CU (ffn_gate) and 32 x 128 below
-  // (attn_q/k, attn_output); Q6_K, whose stages cost more, takes 64 x 128
-  // from half a tile per CU (ffn_down: 141 us against 189) and 32 x 128 below
-  // (attn_v).
-  int cus = 256;
-  if (hipError_t e = compute_units(cus); e != hipSuccess) return e;
-  const int64_t tiles64 = ((M + 63) / 64) * ((N + 127) / 128);
+  a.splits = p.splits;
+  if (p.splits > 1 && partials == nullptr) return hipErrorInvalidValue;
+  hipError_t e;
   if (type == QK_TYPE_Q6_K)
-    return 2 * tiles64 >= cus ? launch_cfg<QK_TYPE_Q6_K, 2, 1>(a, stream)
-                              : launch_cfg<QK_TYPE_Q6_K, 1, 1>(a, stream);
-  return tiles64 >= 2 * cus ? launch_cfg<QK_TYPE_Q4_K, 2, 1>(a, stream)
-                            : launch_cfg<QK_TYPE_Q4_K, 1, 1>(a, stream);
+    e = p.wide ? launch_cfg<QK_TYPE_Q6_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q6_K, 1, 1>(a, stream);
+  else
+    e = p.wide ? launch_cfg<QK_TYPE_Q4_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q4_K, 1, 1>(a, stream);
+  if (e != hipSuccess || p.splits == 1) return e;
+  gemm_kq_reduce_kernel<<<dim3(static_cast<uint32_t>((N + 255) / 256), static_cast<uint32_t>(M)), 256,
+                          0, stream>>>(partials, row_scale, y, static_cast<int>(M),
+                                       static_cast<int>(N), p.splits);
+  return hipGetLastError();
 }
 
 }  // namespace qk

@@ -55,12 +55,13 @@ int matvec_rows_per_launch(int64_t K);
 // Activation rows above which matmul runs as the MFMA GEMM instead of the mat-vec.
 constexpr int64_t kGemvMaxRows = 8;
 
-// Bytes of device scratch launch_gemm needs for M x K activations (their fp16
-// Q8 round trip), rounded up to 256.
-size_t gemm_workspace_bytes(int64_t M, int64_t K);
+// Bytes of device scratch the prefill GEMM needs for M x K activations (their
+// fp16 Q8 round trip, row scales, block sums) and, when the launch splits K,
+// the partial products of an N-column product of this type; rounded up to 256.
+size_t gemm_workspace_bytes(int64_t M, int64_t K, int type, int64_t N);
 
-// workspace (>= gemm_workspace_bytes(M, K), 16-byte aligned) = fp16 of the Q8
-// round trip of x[M x K].
+// workspace (>= gemm_workspace_bytes(M, K, ...), 16-byte aligned) = fp16 of
+// the Q8 round trip of x[M x K], row scales, block sums.
 hipError_t launch_gemm_prep(const float* x, int64_t M, int64_t K, void* workspace,
                             hipStream_t stream);
 
@@ -69,11 +70,13 @@ hipError_t launch_gemm_core(const void* workspace, const void* w, int type, int6
                             float* y, int64_t M, hipStream_t stream);
 
 // The Q4_K / Q6_K GEMM (gemm_kquant.hip) over the prepared planes: hi (lo
-// follows it), row scales and (Q4_K) sub-block sums of the workspace.
+// follows it), row scales and (Q4_K) sub-block sums of the workspace, partial
+// products in `partials` (gemm_kq_partial_bytes of them; unused when 0).
 // gemm_kq_fits: the shape is within its 32-bit tile and row indices.
 bool gemm_kq_fits(int64_t M, int64_t K, int64_t N);
+size_t gemm_kq_partial_bytes(int type, int64_t M, int64_t K, int64_t N);
 hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, const void* xsums,
-                          const void* w, int64_t K, int64_t N, float* y, int64_t M,
+                          const void* w, int64_t K, int64_t N, float* y, int64_t M, float* partials,
                           hipStream_t stream);
 
 // Bytes of the argmax workspace (zero-filled once by the caller).

@@ -71,7 +71,7 @@ def stage_k(q6, c):
     return 256 * (c >> 2) + 128 * ((c >> 1) & 1) + 32 * (c & 1) if q6 else STAGE_K * c
 
 
-def run_model(cfg, oracle, qtype, M, N, K, seed):
+def run_model(cfg, oracle, qtype, M, N, K, seed, splits=1):
     S, nst = K // 256, K // STAGE_K
     q6 = qtype == 14
     SB = BYTES[qtype]
@@ -92,7 +92,10 @@ def run_model(cfg, oracle, qtype, M, N, K, seed):
     h, l32 = lane >> 5, lane & 31
     swz = l32 & 15
     tid = np.arange(64 * WAVES)
-    for t in range(tiles):
+    partial = np.zeros((splits, M, N))
+    for u in range(tiles * splits):
+        t, split = u // splits, u % splits
+        sb0, sb1 = split * S // splits, (split + 1) * S // splits
         mt, nt = t // n_tiles, t % n_tiles
         m0, n0 = mt * cfg.BM, nt * cfg.BN
         # activation piece addresses (halves) of every thread
@@ -105,7 +108,7 @@ def run_model(cfg, oracle, qtype, M, N, K, seed):
             pa.append(np.where(piece >> 3 == 1, M * K, 0) + np.minimum(m0 + row, M - 1) * K + koff)
         acc = np.zeros((WAVES, cfg.TM, cfg.TN, 32, 32))
         ph = np.zeros_like(acc)
-        for sb in range(S):
+        for sb in range(sb0, sb1):
             min_b = np.zeros((WAVES, cfg.TN, 64, 8))
             for g in range(4):
                 c = 4 * sb + g
@@ -201,17 +204,22 @@ def run_model(cfg, oracle, qtype, M, N, K, seed):
                         for nn in range(32):
                             n = n0 + wv * 32 * cfg.TN + 32 * j + nn
                             if n < N:
-                                y[m, n] = acc[wv, i, j, mm, nn] * scale[m]
+                                partial[split, m, n] = acc[wv, i, j, mm, nn]
                                 seen[m, n] += 1
-    assert np.all(seen == 1), "every output written exactly once"
+    assert np.all(seen == splits), "every output written once per split"
+    y = partial[0]
+    for k in range(1, splits):  # the reduce kernel adds the splits in order
+        y = y + partial[k]
+    y = y * scale[:, None].astype(np.float64)
     ref = oracle.reference_product(x, w, qtype, K, N)
     return y, np.asarray(ref, np.float64).reshape(M, N)
 
 
 @pytest.mark.parametrize("qtype", [12, 14])
 @pytest.mark.parametrize("TM,TN", [(2, 1), (1, 1)])  # the two tiles the launcher uses
-def test_gemm_model_matches_oracle(oracle, qtype, TM, TN):
-    y, ref = run_model(Cfg(TM, TN), oracle, qtype, M=70, N=300, K=768, seed=91)
+@pytest.mark.parametrize("K,splits", [(768, 1), (1024, 3)])
+def test_gemm_model_matches_oracle(oracle, qtype, TM, TN, K, splits):
+    y, ref = run_model(Cfg(TM, TN), oracle, qtype, M=70, N=300, K=K, seed=91, splits=splits)
     err = oracle.row_norm_error(y, ref)
     print(f"row-norm error {err:.3e}")
     assert err <= 1e-6
