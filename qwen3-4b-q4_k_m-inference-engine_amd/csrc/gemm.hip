@@ -55,13 +55,25 @@ __device__ __forceinline__ void prep_group(const f32x4 a, const f32x4 b, float u
                          0, __builtin_bit_cast(int, bmax), 0xB1, 0xF, 0xF, false)));
   bmax = fmaxf(bmax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
                          0, __builtin_bit_cast(int, bmax), 0x4E, 0xF, 0xF, false)));
-  const float scale = bmax / 127.0f;
+  // codes round(x/amax*127) and scale amax/127 as the reference computes them
+  // in float: for amax in [2^-64, 2^64] through the exact reciprocal and
+  // Markstein quotient of the mat-vec quantiser (equal to IEEE division)
+  float code[8], scale;
+  if (bmax >= 0x1p-64f && bmax <= 0x1p64f) {
+    const float r = refined_rcp(bmax);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) code[i] = static_cast<float>(round_code(markstein_div(v[i], bmax, r) * 127.0f));
+    scale = markstein_div(bmax, 127.0f, 1.0f / 127.0f);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) code[i] = bmax == 0.0f ? 0.0f : roundf((v[i] / bmax) * 127.0f);
+    scale = bmax / 127.0f;
+  }
   uint32_t h[4], l[4];
   float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float c0 = bmax == 0.0f ? 0.0f : roundf((v[2 * i] / bmax) * 127.0f);
-    const float c1 = bmax == 0.0f ? 0.0f : roundf((v[2 * i + 1] / bmax) * 127.0f);
+    const float c0 = code[2 * i], c1 = code[2 * i + 1];
     const float s0 = (c0 * scale) * up, s1 = (c1 * scale) * up;
     split2(s0, s1, h[i], l[i]);
     sum += s0;
