@@ -2,50 +2,51 @@
 // with integer-structured weight operands.
 //
 // Replaces project<Q4_K/Q6_K> launched with gridDim.y = rows
-// (src/cuda/matmul.cu:151-158).
+// (src/cuda/matmul.cu:151-158). The activations arrive prepared (gemm.hip,
+// prep_rows_kernel): v = 2^s(m) x8 with x8 the Q8 round trip of x
+// (MatmulReference.hpp:11-29), held as fp16 planes hi + lo (22 significant
+// bits), and for Q4_K X[m,j] = 2^-5 * (sum of v over 32-value block j), also
+// as hi + lo. Every MFMA (v_mfma_f32_32x32x16_f16, fp32 accumulation) takes an
+// activation plane as A and an exact fp16 integer weight operand as B:
 //
-// Q6_K (w = d*sc*q, q in -32..31, sc int8; src/cuda/embedding.cu:34-59): the
-// weight operand is sc*q, |sc*q| <= 4096, held as B_hi = fp16(sc*q) and the
-// exact remainder B_lo = sc*q - B_hi in {-1, 0, 1} (fp16 integers are exact
-// to 2048, even numbers to 4096), so a step is hi*B_hi + lo*B_hi + hi*B_lo
-// and d folds in once per superblock; no min term. A stage is 64 weights of
-// one half (128 weights) of the superblock: groups a and a+2 (a = stage & 1),
-// which share the qh bytes; a lane takes l = 16h .. 16h+15 of both.
+// Q4_K (w = d*sc_j*q - dmin*m_j, src/cuda/embedding.cu:6-32): each superblock
+// of a weight row adds d * sum_k v*(sc_j*q) - 32*dmin * sum_j m_j*X_j to
+// 2^s*y. sc_j*q <= 63*15 is exact in fp16, so a 16-deep step is hi*B + lo*B;
+// d and dmin fold in once per superblock and the min term is one more MFMA
+// per superblock (A = X hi in k 0-7 and X lo in k 8-15, B = m_j in both).
 //
-// Q4_K:
-// With w = d*sc_j*q - dmin*m_j (src/cuda/embedding.cu:6-32) and x8 the Q8 round
-// trip of x (MatmulReference.hpp:11-29), each superblock of a weight row adds
-//     d * sum_k v[m,k] * (sc_j*q)[n,k]  -  32*dmin * sum_j m_j * X[m,j]
-// to 2^s(m) * y[m,n], where (gemm.hip, prep_rows_kernel)
-//   v = 2^s x8, held as fp16 planes hi + lo (22 significant bits),
-//   X[m,j] = 2^-5 * (sum of v over sub-block j), also as hi + lo.
-// sc_j*q <= 63*15 is an exact fp16 integer, so every 16-deep MFMA step is
-// hi*B + lo*B with one unsplit weight operand and no per-block scaling; d
-// and dmin fold in once per superblock and the min term is one more MFMA per
-// superblock (A = X hi in k 0-7 and X lo in k 8-15, B = m_j in both halves).
+// Q6_K (w = d*sc*q, q in -32..31, sc int8, src/cuda/embedding.cu:34-59):
+// |sc*q| <= 4096, past the 2048 up to which fp16 integers are exact, so the
+// operand is B_hi = fp16(sc*q) plus the exact remainder B_lo = sc*q - B_hi in
+// {-1, 0, 1}: a step is hi*B_hi + lo*B_hi + hi*B_lo; d folds in once per
+// superblock.
 //
 // Workgroup: 4 waves side by side in N, each owning TM x TN tiles of 32 x 32
 // of the (BM = 32 TM) x (BN = 128 TN) output tile. K runs in stages of 64
-// weights (one 32-byte qs group: sub-blocks 2g, 2g+1 of a superblock):
-//   - the activation tile of a stage (BM rows x hi/lo x 64 halves) goes
-//     through one of two LDS slots: the workgroup loads stage c+2 into
-//     registers while it computes stage c and writes stage c+1 (loaded a
-//     stage earlier) in the middle of it; one barrier per stage;
-//   - each lane loads its own weight bytes into registers (its 16 qs bytes
-//     a stage ahead, the superblock header during the superblock before)
-//     and its sub-block sums once per superblock: no weight tile in LDS.
+// weights. Q4_K stage g of a superblock is its qs group g (sub-blocks 2g and
+// 2g+1, low and high nibbles); Q6_K stage g is groups a and a+2 (a = g & 1)
+// of half g / 2, which share their qh bytes.
+//   - The activation tile of a stage (BM rows x hi/lo x the stage's 64
+//     halves) goes through one of two LDS slots: the workgroup loads stage
+//     c+2 into registers while it computes stage c and writes stage c+1
+//     (loaded a stage earlier) in the middle of it; one barrier per stage.
+//   - Each lane loads its own weight bytes into registers (a stage's 16 qs,
+//     or 16 ql + 16 qh, bytes a stage ahead; a superblock's header or scales
+//     and d during the superblock before) and, for Q4_K, its block sums once
+//     per superblock: no weight tile passes through LDS.
+//   - A grid of few tiles with a deep K splits K into superblock ranges;
+//     gemm_kq_reduce_kernel adds the partial tiles in split order.
 // Rows past M or N are clamped to the last row on load and not stored.
 //
-// MFMA operand rule (v_mfma_f32_32x32x16_f16, checked on the device): lane l
-// gives row l%32 of A and column l%32 of B with the same 8 k values, half-wave
-// l/32 choosing which 8; D lane l, register r holds row 8*(r/4) + 4*(l/32) +
-// r%4, column l%32. The k order inside a step is free as long as A and B
-// agree: in step (u, s) of a stage, half-wave h takes the 8 weights at
-// qs bytes 16h + 8s .. +7 of the group, nibble u (sub-block 2g + u), i.e.
-// stage-local k = 32u + 16h + 8s + e. An A slot row is 256 bytes: the 8
-// hi and 8 lo 16-byte pieces, piece L = 8*plane + p stored at position
-// L ^ (row & 15), so the 16 rows a ds_read_b128 serves at once hit 16
-// different bank groups.
+// MFMA operand rule (checked on the device): lane l gives row l%32 of A and
+// column l%32 of B with the same 8 k values, half-wave l/32 choosing which 8;
+// D lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32. The k
+// order inside a step is free as long as A and B agree: in step (u, s) of a
+// stage, half-wave h takes weights l = 16h + 8s .. +7 of its 32-weight group
+// u (Q4_K: qs bytes 16h + 8s .. +7, nibble u; Q6_K: group a + 2u). An A slot
+// row is 256 bytes, the 8 hi and 8 lo 16-byte pieces, piece L = 8*plane + p
+// at position L ^ (row & 15), so the 16 rows a ds_read_b128 serves at once
+// hit 16 different bank groups.
 #include <algorithm>
 
 #include "qk_device.hpp"
