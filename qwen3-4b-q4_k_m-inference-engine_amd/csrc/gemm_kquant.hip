@@ -492,7 +492,10 @@ KQPlan plan(int type, int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = wide ? tiles64 : tiles32;
   const int64_t by_grid = std::clamp<int64_t>(2 * kPlanCUs / tiles, 1, 4);
   const int64_t by_depth = std::max<int64_t>(K / 256 / 8, 1);
-  return {wide, static_cast<int>(std::min(by_grid, by_depth))};
+  // (fewer than 512 tiles also keeps M below 16384, inside the reduce grid's
+  // 65535 rows; the check states it)
+  const bool fits_reduce = M <= 65535;
+  return {wide, fits_reduce ? static_cast<int>(std::min(by_grid, by_depth)) : 1};
 }
 
 }  // namespace
