@@ -122,6 +122,17 @@ int qk_matmul_segments(const float *x, int64_t M, int64_t K, const qk_segment *s
 int qk_ffn_gate_up(const float *x, const void *gate, const void *up, int type, int64_t K,
                    int64_t N, float *h, int64_t M, qk_stream_t stream);
 
+/* qk_ffn_gate_up on RMSNorm(x): each row x_m is first replaced by
+ * (x_m * rsqrt(mean(x_m^2) + eps)) * norm (norm: K device floats). Replaces
+ * rms_norm(ffn_norm) before the FFN (src/Engine.cpp:97-99,
+ * src/cuda/rms_norm.cu:6-24,28-36). M = 1: the norm is folded into the one
+ * launch and the normalised row never goes to memory; other M: the norm runs
+ * first into stream-ordered scratch. eps must be > 0 (QK_ERR_INVALID_ARGUMENT
+ * otherwise, as the reference throws); M = 0 does nothing. */
+int qk_ffn_gate_up_norm(const float *x, const float *norm, float eps, const void *gate,
+                        const void *up, int type, int64_t K, int64_t N, float *h, int64_t M,
+                        qk_stream_t stream);
+
 /* Bytes of the workspace qk_argmax / qk_matmul_argmax need. The caller
  * zero-fills it once before its first use (qk_memset_async or hipMemset);
  * every call leaves it ready for the next. Calls that may run concurrently

@@ -384,6 +384,23 @@ void qko_silu_multiply(const float *gate, const float *up, float *out, int64_t c
     }
 }
 
+/* src/cuda/rms_norm.cu:6-24: out = x * rsqrt(mean(x^2) + eps) * scale per
+ * row of `width` values, products left to right in float. The sum of squares
+ * is accumulated in double (the reference's per-thread float sums and tree
+ * reduction, and its approximate rsqrtf, are not restated: they move the
+ * result by a few ulp) and 1/sqrt is taken in double, then rounded. */
+void qko_rms_norm(const float *x, const float *scale, float *out, int64_t rows, int64_t width,
+                  float eps)
+{
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * width;
+        double sum = 0.0;
+        for (int64_t i = 0; i < width; ++i) sum += (double)xr[i] * (double)xr[i];
+        const float inv = (float)(1.0 / sqrt((double)(float)(sum / (double)width) + (double)eps));
+        for (int64_t i = 0; i < width; ++i) out[r * width + i] = (xr[i] * inv) * scale[i];
+    }
+}
+
 /* src/cuda/argmax.cu:25-98: the candidate starts at (SIZE_MAX, -inf) (:13-15)
  * and is replaced only by a strictly greater score (:32), ties across threads
  * going to the lower index (:19-23): the first index of the largest value;

@@ -71,6 +71,8 @@ int qko_integer_product(const float *x, const void *w, int type, int64_t K, int6
 
 /* out = gate/(1+exp(-gate)) * up (src/cuda/silu_multiply.cu:6-12). */
 void qko_silu_multiply(const float *gate, const float *up, float *out, int64_t count);
+void qko_rms_norm(const float *x, const float *scale, float *out, int64_t rows, int64_t width,
+                  float eps);
 /* Index of the largest value; ties resolve to the lowest index (src/cuda/argmax.cu:25-98). */
 int64_t qko_argmax(const float *v, int64_t count);
 

@@ -39,6 +39,7 @@ _SIGS = {
     "qko_reference_product_f32": ([_P, _P, _int, _i64, _i64, _i64, _P, _int], _int),
     "qko_integer_product": ([_P, _P, _int, _i64, _i64, _i64, _P], _int),
     "qko_silu_multiply": ([_P, _P, _P, _i64], None),
+    "qko_rms_norm": ([_P, _P, _P, _i64, _i64, ctypes.c_float], None),
     "qko_argmax": ([_P, _i64], _i64),
     "qko_mix64": ([_u64], _u64),
     "qko_word": ([_u64, _u64], _u64),
@@ -150,6 +151,15 @@ def silu_multiply(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     up = np.ascontiguousarray(up, dtype=np.float32)
     out = np.empty_like(gate)
     load().qko_silu_multiply(_c(gate), _c(up), _c(out), gate.size)
+    return out
+
+
+def rms_norm(x: np.ndarray, scale: np.ndarray, width: int, eps: float) -> np.ndarray:
+    """src/cuda/rms_norm.cu:6-24 per row of `width` values (qko_rms_norm)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    scale = np.ascontiguousarray(scale, dtype=np.float32)
+    out = np.empty_like(x)
+    load().qko_rms_norm(_c(x), _c(scale), _c(out), x.size // width, width, eps)
     return out
 
 

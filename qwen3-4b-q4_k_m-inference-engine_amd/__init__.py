@@ -65,6 +65,8 @@ _SIGNATURES = {
     "qk_matmul_segments": [_c_void_p, _i64, _i64, ctypes.POINTER(Segment), _int, _c_void_p],
     "qk_ffn_gate_up": [_c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _i64,
                        _c_void_p],
+    "qk_ffn_gate_up_norm": [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _int, _i64, _i64,
+                            _c_void_p, _i64, _c_void_p],
     "qk_argmax_workspace_size": [],
     "qk_argmax": [_c_void_p, _i64, _c_void_p, _c_void_p, _size, _c_void_p],
     "qk_matmul_argmax": [_c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
@@ -333,6 +335,13 @@ def ffn_gate_up(x, gate, up, qtype: int, K: int, N: int, h, M: int, stream=None)
     """h = SiLU(x . gate^T) * (x . up^T) (qk_ffn_gate_up)."""
     check(load().qk_ffn_gate_up(_ptr(x), _ptr(gate), _ptr(up), qtype, K, N, _ptr(h), M,
                                 _stream_ptr(stream)))
+
+
+def ffn_gate_up_norm(x, norm, eps: float, gate, up, qtype: int, K: int, N: int, h, M: int,
+                     stream=None) -> None:
+    """h = SiLU(n . gate^T) * (n . up^T), n = RMSNorm(x) with scale `norm` (qk_ffn_gate_up_norm)."""
+    check(load().qk_ffn_gate_up_norm(_ptr(x), _ptr(norm), eps, _ptr(gate), _ptr(up), qtype, K, N,
+                                     _ptr(h), M, _stream_ptr(stream)))
 
 
 def matmul_workspace_size(qtype: int, K: int, N: int, M: int) -> int:

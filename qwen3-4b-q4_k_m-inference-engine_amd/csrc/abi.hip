@@ -258,6 +258,49 @@ int qk_ffn_gate_up(const float* x, const void* gate, const void* up, int type, i
   return run_matvec(p, M, K, 1, as_stream(stream));
 }
 
+int qk_ffn_gate_up_norm(const float* x, const float* norm, float eps, const void* gate, const void* up,
+                        int type, int64_t K, int64_t N, float* h, int64_t M, qk_stream_t stream) {
+  const int status = validate_matmul(type, K, N, M);
+  if (status != QK_OK) return status;
+  if (M == 0) return QK_OK;  // src/cuda/rms_norm.cu:31
+  if (!(eps > 0.0f))        // src/cuda/rms_norm.cu:32
+    return fail(QK_ERR_INVALID_ARGUMENT, "RMSNorm requires a positive epsilon");
+  if (!x || !norm || !gate || !up || !h)
+    return fail(QK_ERR_INVALID_ARGUMENT, "ffn pointers must be non-null");
+  for (const void* w : {gate, up}) {
+    const int status = validate_weight_pointer(w, type);
+    if (status != QK_OK) return status;
+  }
+  qk::MatvecParams p = params_for(x, nullptr);
+  p.nseg = 2;
+  p.h = h;
+  p.seg[0] = {static_cast<const uint8_t*>(gate), nullptr, static_cast<int32_t>(N), type, 0, 0};
+  p.seg[1] = {static_cast<const uint8_t*>(up), nullptr, static_cast<int32_t>(N), type, 0, 0};
+  const hipStream_t s = as_stream(stream);
+  if (M == 1) {  // the norm folded into the whole-share kernel's prologue
+    p.M = 1;
+    p.K = static_cast<int32_t>(K);
+    p.S = static_cast<int32_t>(K / 256);
+    p.norm = norm;
+    p.eps = eps;
+    bool launched = false;
+    const hipError_t error = qk::launch_stream_matvec(p, 3, s, launched);
+    if (error != hipSuccess) return hip_fail(error, "matmul launch failed");
+    if (launched) return QK_OK;
+  }
+  // Otherwise the norm runs on its own into stream-ordered scratch, then the
+  // fused gate/up product.
+  float* normalized = nullptr;
+  hipError_t error = hipMallocAsync(reinterpret_cast<void**>(&normalized),
+                                    static_cast<size_t>(M * K) * sizeof(float), s);
+  if (error != hipSuccess) return hip_fail(error, "RMSNorm scratch allocation failed");
+  error = qk::launch_rms_norm(x, norm, normalized, M, K, eps, s);
+  int result = error == hipSuccess ? QK_OK : hip_fail(error, "RMSNorm launch failed");
+  if (result == QK_OK) result = qk_ffn_gate_up(normalized, gate, up, type, K, N, h, M, stream);
+  (void)hipFreeAsync(normalized, s);
+  return result;
+}
+
 size_t qk_argmax_workspace_size(void) { return qk::argmax_workspace_bytes(); }
 
 int qk_argmax(const float* logits, int64_t count, uint32_t* result, void* workspace,

@@ -33,6 +33,11 @@ StreamKernel stream_kernel_j(int J) {
 }
 
 StreamKernel stream_kernel(int type, int J, int mode) {
+  if (mode == 3) {
+    if (type == QK_TYPE_Q4_K) return stream_kernel_j<QK_TYPE_Q4_K, 3>(J);
+    if (type == QK_TYPE_Q6_K) return stream_kernel_j<QK_TYPE_Q6_K, 3>(J);
+    return nullptr;
+  }
   if (mode == 1) {
     if (type == QK_TYPE_Q4_K) return stream_kernel_j<QK_TYPE_Q4_K, 1>(J);
     if (type == QK_TYPE_Q6_K) return stream_kernel_j<QK_TYPE_Q6_K, 1>(J);
@@ -167,14 +172,16 @@ hipError_t launch_stream_mt(const MatvecParams& p, int mode, hipStream_t stream,
 
 hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t stream, bool& launched) {
   launched = false;
-  if (p.x == nullptr || (mode != 0 && mode != 1) || p.M > 8) return hipSuccess;
+  if (p.x == nullptr || (mode != 0 && mode != 1 && mode != 3) || p.M > 8) return hipSuccess;
+  if (mode == 3 && (p.M != 1 || p.norm == nullptr)) return hipSuccess;  // the fold is M = 1 only
   if (p.M > 1) return launch_stream_mt(p, mode, stream, launched);
   if (p.K > kStreamMaxK) return hipSuccess;
   int cus = 0, max_lds = 0;
   hipError_t e = device_limits(cus, max_lds);
   if (e != hipSuccess) return e;
-  const int nseg = mode == 1 ? 1 : p.nseg;
-  const int parts = mode == 1 ? 2 : 1, wpp = kStreamWaves / parts;
+  const bool ffn = mode == 1 || mode == 3;
+  const int nseg = ffn ? 1 : p.nseg;
+  const int parts = ffn ? 2 : 1, wpp = kStreamWaves / parts;
   const int64_t S = p.S;
 
   int count[kMaxSegments] = {0};
@@ -186,6 +193,8 @@ hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t str
   sp.K = p.K;
   sp.S = p.S;
   sp.nseg = nseg;
+  sp.norm = p.norm;
+  sp.eps = p.eps;
   int J = 0, type = 0, begin = 0;
   int64_t max_sb = 0;
   bool q4 = false, q6 = false;
@@ -201,7 +210,7 @@ hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t str
                  p.seg[j].rows / count[j], p.seg[j].rows % count[j], 0};
     begin += count[j];
   }
-  if (mode == 1) sp.seg[1] = {p.seg[1].w, nullptr, p.seg[1].rows, p.seg[1].type, 0, 0, 0, 0};
+  if (ffn) sp.seg[1] = {p.seg[1].w, nullptr, p.seg[1].rows, p.seg[1].type, 0, 0, 0, 0};
   if (J > kStreamMaxJ) return hipSuccess;
   type = q4 && q6 ? 0 : q4 ? QK_TYPE_Q4_K : QK_TYPE_Q6_K;
   sp.max_sb = static_cast<int32_t>(max_sb);

@@ -47,7 +47,10 @@ struct StreamSegment {
 struct StreamParams {
   const float* x;
   float* h;
+  const float* norm;  // MODE 3: RMSNorm scale [K] applied to x before the Q8 round trip
   int32_t K, S, nseg, max_sb;  // max_sb: superblocks of the largest workgroup share (per part)
+  float eps;                   // MODE 3: RMSNorm epsilon
+  int32_t pad0, pad1, pad2;
   StreamSegment seg[kMaxSegments];
 };
 
@@ -199,17 +202,24 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
 // superblock are a runtime value), so the loads of both types are issued by
 // the same straight-line code and the quantiser's waits count them exactly;
 // only the consumption is specialised per type.
+// MODE 0: y_j = x . W_j^T per segment; 1: h = SiLU(x . gate^T) * (x . up^T);
+// 3: mode 1 on RMSNorm(x) (src/cuda/rms_norm.cu:6-24 folded into the
+// prologue: the quantiser waves also stage the norm scale, take the row's
+// sum of squares once the weight loads are out, and quantise
+// (x * rsqrt(mean(x^2) + eps)) * scale).
 template <int TYPE, int J, int MODE>
 __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const StreamParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
-  constexpr int kParts = MODE == 1 ? 2 : 1;
+  constexpr bool kFfn = MODE == 1 || MODE == 3;
+  constexpr int kParts = kFfn ? 2 : 1;
   constexpr int kWpp = kStreamWaves / kParts;  // waves per part
   // Every argument in one scalar-load round (see matvec_kernel).
 #pragma unroll
   for (int j = 0; j < kMaxSegments; ++j)
     asm volatile("" ::"s"(p.seg[j].w), "s"(p.seg[j].y), "s"(p.seg[j].rows), "s"(p.seg[j].type),
                  "s"(p.seg[j].wg_begin), "s"(p.seg[j].per), "s"(p.seg[j].rem), "s"(p.seg[j].pad));
-  asm volatile("" ::"s"(p.x), "s"(p.h), "s"(p.K), "s"(p.S), "s"(p.nseg), "s"(p.max_sb));
+  asm volatile("" ::"s"(p.x), "s"(p.h), "s"(p.norm), "s"(p.K), "s"(p.S), "s"(p.nseg), "s"(p.max_sb),
+               "s"(p.eps), "s"(p.pad0), "s"(p.pad1), "s"(p.pad2));
   __builtin_amdgcn_sched_barrier(0);
   const int K = p.K, nseg = p.nseg;
 
@@ -217,8 +227,11 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   const int nq = quantiser_waves<1>(K / 8);
   const int lane = static_cast<int>(threadIdx.x & 63u);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  XStage<1> stage;
-  if (wave < nq) stage_x<1>(p.x, 1, K, nq, stage);
+  XStage<1> stage, nstage;  // nstage: MODE 3's norm scale of the staged tasks
+  if (wave < nq) {
+    stage_x<1>(p.x, 1, K, nq, stage);
+    if constexpr (MODE == 3) stage_x<1>(p.norm, 1, K, nq, nstage);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   const int wg = static_cast<int>(blockIdx.x);
@@ -240,7 +253,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   // arguments, the compiler re-reads them from memory there (a round trip).
   int S = p.S, max_sb = p.max_sb;
   float* hout = p.h;
-  asm volatile("" : "+s"(S), "+s"(max_sb), "+s"(hout), "+s"(yout), "+s"(r0), "+s"(r1));
+  float eps = p.eps;
+  asm volatile("" : "+s"(S), "+s"(max_sb), "+s"(hout), "+s"(yout), "+s"(r0), "+s"(r1), "+s"(eps));
 
   // The wave's run [sb_a, sb_b) as 16-byte chunks. An idle wave reads the
   // workgroup's first chunk. The last chunk of the matrix is moved back so it
@@ -255,7 +269,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   const int nsb = (r1 - r0) * S;  // superblocks of the workgroup, per part
   ws.sb_a = nsb * wv / kWpp;
   ws.sb_b = nsb * (wv + 1) / kWpp;
-  const uint8_t* w = MODE == 1 && ws.part ? p.seg[1].w : w0;
+  const uint8_t* w = kFfn && ws.part ? p.seg[1].w : w0;
   const int64_t row_bytes = static_cast<int64_t>(S) * B;
   const uint8_t* run = w + r0 * row_bytes + static_cast<int64_t>(ws.sb_b > ws.sb_a ? ws.sb_a : 0) * B;
   ws.o = static_cast<int>(reinterpret_cast<uintptr_t>(run) & 3u);  // 0 or 2 (Q6_K), 0 (Q4_K)
@@ -276,6 +290,37 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   lds_q8_block* xq = (lds_q8_block*)(lds_raw);
   lds_u8* wlds = (lds_u8*)(lds_raw) + S * 8 * static_cast<int>(sizeof(qk_q8_block));
   lds_f32* sums = reinterpret_cast<lds_f32*>(wlds + kStreamWaves * J * 1024);
+  if constexpr (MODE == 3) {
+    // the row's sum of squares: lanes, then waves in order (one barrier);
+    // the wave partials sit in the weight staging area, unused until the
+    // consume loop, which starts after the next barrier
+    lds_f32* norm_part = reinterpret_cast<lds_f32*>(wlds);
+    float ss = 0.0f;
+    if (wave < nq) {
+#pragma unroll
+      for (int i = 0; i < kXStaged; ++i) {
+        const int t = static_cast<int>(threadIdx.x) + 64 * nq * i;
+        const f32x4 a = stage.a[i], b = stage.b[i];
+        if (t < K / 8)
+          ss += ((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w)) +
+                ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
+      }
+    }
+    ss = row_lanes_sum<64>(ss);  // DPP and lane swaps: no LDS round trips
+    if (lane == 0) norm_part[wave] = ss;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kStreamWaves; ++i) total += norm_part[i];
+    const float inv = rsqrtf(total / static_cast<float>(K) + eps);
+    if (wave < nq) {
+#pragma unroll
+      for (int i = 0; i < kXStaged; ++i) {
+        stage.a[i] = (stage.a[i] * inv) * nstage.a[i];
+        stage.b[i] = (stage.b[i] * inv) * nstage.b[i];
+      }
+    }
+  }
   if (wave < nq) quantize_staged_into_lds<1>(1, K, nq, stage, xq);  // K <= kStreamMaxK: all staged
   __syncthreads();
 
@@ -284,12 +329,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   global_f32* gh = (global_f32*)(hout);
 
   if constexpr (TYPE != 0) {
-    stream_consume<TYPE, J, MODE, false>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums);
+    stream_consume<TYPE, J, kFfn ? 1 : MODE, false>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums);
   } else {
     if (type == QK_TYPE_Q4_K)
-      stream_consume<QK_TYPE_Q4_K, J, MODE, true>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums);
+      stream_consume<QK_TYPE_Q4_K, J, kFfn ? 1 : MODE, true>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums);
     else
-      stream_consume<QK_TYPE_Q6_K, J, MODE, true>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums);
+      stream_consume<QK_TYPE_Q6_K, J, kFfn ? 1 : MODE, true>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums);
   }
 }
 

@@ -33,6 +33,9 @@ struct MatvecParams {
   int32_t rows_total;           // rows of all segments (FFN mode: of gate)
   int32_t split_wg, split_row;  // mixed types: workgroups / rows of the Q4_K part
   int32_t pad;
+  const float* norm;            // FFN-with-norm mode (3): RMSNorm scale [K]
+  float eps;                    // its epsilon
+  int32_t pad2;
   void* argmax_ws;              // argmax mode: ArgmaxWorkspace (argmax.hpp)
   uint32_t* argmax_result;      // argmax mode: index of the largest output
   MatvecSegment seg[kMaxSegments];
@@ -91,6 +94,10 @@ hipError_t launch_quantize_q8(const float* x, int64_t M, int64_t K, qk_q8_block*
 
 hipError_t launch_dequantize_rows(const void* packed, float* out, int64_t rows, int64_t K,
                                   size_t row_bytes, int type, hipStream_t stream);
+
+// out[rows x width] = RMSNorm of x with per-column scale (src/cuda/rms_norm.cu:6-24).
+hipError_t launch_rms_norm(const float* x, const float* scale, float* out, int64_t rows,
+                           int64_t width, float eps, hipStream_t stream);
 
 hipError_t launch_silu_multiply(const float* gate, const float* up, float* out, int64_t count,
                                 hipStream_t stream);

@@ -106,6 +106,15 @@ def test_other_validation(qk):
     assert lib.qk_ffn_gate_up(None, None, None, 12, 2560, 0, None, 1, None) == 1
     assert lib.qk_ffn_gate_up(None, None, None, 12, 2560, 8, None, 0, None) == 0
     assert lib.qk_ffn_gate_up(None, None, None, 12, 2560, 8, None, 1, None) == 1  # null pointers
+    # the RMSNorm fold: the reference's `!(epsilon > 0)` check (src/cuda/rms_norm.cu:32)
+    p16 = ctypes.c_void_p(16)
+    assert lib.qk_ffn_gate_up_norm(p16, p16, 0.0, p16, p16, 12, 2560, 8, p16, 1, None) == 1
+    assert b"epsilon" in lib.qk_last_error()
+    assert lib.qk_ffn_gate_up_norm(p16, p16, float("nan"), p16, p16, 12, 2560, 8, p16, 1, None) == 1
+    assert lib.qk_ffn_gate_up_norm(p16, None, 1e-6, p16, p16, 12, 2560, 8, p16, 1, None) == 1
+    assert lib.qk_ffn_gate_up_norm(p16, p16, 1e-6, p16, p16, 13, 2560, 8, p16, 1, None) == 2
+    assert lib.qk_ffn_gate_up_norm(p16, p16, 1e-6, p16, p16, 12, 2500, 8, p16, 1, None) == 1
+    assert lib.qk_ffn_gate_up_norm(None, None, 0.0, None, None, 12, 2560, 8, None, 0, None) == 0
 
 
 def test_argmax_validation_on_the_host(qk):

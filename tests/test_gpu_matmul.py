@@ -334,6 +334,40 @@ def test_ffn_gate_up_silu(gpu, oracle, qtype, M):
     assert oracle.row_norm_error(got, sep.download(np.float32).reshape(M, N).astype(np.float64)) <= 1e-6
 
 
+@pytest.mark.parametrize("qtype", [Q4, Q6])
+@pytest.mark.parametrize("M", [1, 3, 9])
+def test_ffn_gate_up_norm(gpu, oracle, qtype, M):
+    """ffn_norm then SiLU(gate) * up (src/Engine.cpp:97-100): M = 1 folds the norm
+    into the one launch, other M run the norm kernel first."""
+    K, N, eps = 2560, 9728, 1e-6
+    gate = make_weight(gpu, oracle, qtype, N, K, SEED + 710)
+    up = make_weight(gpu, oracle, qtype, N, K, SEED + 711)
+    x = oracle.synth_normal(M * K, SEED + 712) * np.float32(7.0)  # rows far from unit RMS
+    x[:K][::5] *= np.float32(40.0)                                # a few large entries
+    scale = (np.float32(1.0) + np.float32(0.3) * oracle.synth_normal(K, SEED + 713)).astype(np.float32)
+    xd, sd = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer.from_array(scale)
+    h = gpu.DeviceBuffer(4 * M * N)
+    gpu.ffn_gate_up_norm(xd, sd, eps, gate, up, qtype, K, N, h, M)
+    gpu.synchronize()
+    got = h.download(np.float32).reshape(M, N)
+    n = oracle.rms_norm(x, scale, K, eps)
+    g = oracle.reference_product(n, gate.download(np.uint8), qtype, K, N)
+    u = oracle.reference_product(n, up.download(np.uint8), qtype, K, N)
+    ref = (g / (1.0 + np.exp(-g))) * u
+    err = oracle.row_norm_error(got, ref)
+    print(f"ffn+norm M={M} row-norm error {err:.3e}")
+    # The normalised row may differ from the oracle's in its last bit (another
+    # sum order), which can move one Q8 code of the round trip by a step: about
+    # 7e-4 of the row norm here, so the bar is the path's 1e-3 (measured: no
+    # code moved for these seeds, errors near 2e-8).
+    assert err <= 1e-3
+    # against the unfused FFN on the oracle's normalised rows
+    nd, h2 = gpu.DeviceBuffer.from_array(n), gpu.DeviceBuffer(4 * M * N)
+    gpu.ffn_gate_up(nd, gate, up, qtype, K, N, h2, M)
+    gpu.synchronize()
+    assert oracle.row_norm_error(got, h2.download(np.float32).reshape(M, N).astype(np.float64)) <= 1e-3
+
+
 def test_prologue_quantisation_matches_quantize_kernel(gpu, oracle):
     """The in-kernel Q8 (reciprocal + correction) equals the IEEE-division quantize
     kernel on wide-range data with many exact rounding ties."""

@@ -323,3 +323,26 @@ def test_argmax_follows_the_reference_candidate_rules(oracle):
     for _ in range(20):
         v = rng.integers(-3, 4, 1000).astype(np.float32)   # many ties
         assert oracle.argmax(v) == int(np.argmax(v))       # numpy: first maximal index
+
+
+def test_rms_norm_oracle(oracle):
+    """qko_rms_norm (src/cuda/rms_norm.cu:6-24) pinned by a float64
+    restatement, a closed form and two invariants: a constant row a gives
+    a / sqrt(a^2 + eps) * w; rows come out with unit RMS (w = 1, small eps);
+    eps dominating a tiny row leaves it almost unscaled by the mean."""
+    rng = np.random.default_rng(5)
+    width, rows, eps = 2560, 3, 1e-6
+    x = rng.standard_normal(rows * width).astype(np.float32) * 3.0
+    w = rng.uniform(0.5, 1.5, width).astype(np.float32)
+    got = oracle.rms_norm(x, w, width, eps).reshape(rows, width)
+    xr = x.reshape(rows, width).astype(np.float64)
+    ref = xr / np.sqrt(np.mean(xr * xr, axis=1, keepdims=True) + eps) * w.astype(np.float64)
+    assert np.max(np.abs(got - ref) / np.abs(ref).max()) < 1e-6
+    ones = np.ones(width, np.float32)
+    unit = oracle.rms_norm(x, ones, width, eps).reshape(rows, width).astype(np.float64)
+    assert np.allclose(np.sqrt(np.mean(unit * unit, axis=1)), 1.0, rtol=1e-5)
+    const = oracle.rms_norm(np.full(width, 2.0, np.float32), w, width, 0.25)
+    assert np.allclose(const, 2.0 / np.sqrt(4.25) * w, rtol=1e-6)
+    tiny = np.full(width, 1e-4, np.float32)
+    out = oracle.rms_norm(tiny, ones, width, 1.0)  # mean 1e-8 << eps = 1
+    assert np.allclose(out, 1e-4 / np.sqrt(1.0 + 1e-8), rtol=1e-6)

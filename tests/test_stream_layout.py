@@ -19,8 +19,8 @@ def launcher(rows, types, K, mode):
     S = K // 256
     if K > MAX_K:
         return None
-    nseg = 1 if mode == 1 else len(rows)
-    parts = 2 if mode == 1 else 1
+    nseg = 1 if mode in (1, 3) else len(rows)
+    parts = 2 if mode in (1, 3) else 1
     wpp = WAVES // parts
     byt = [rows[j] * S * BYTES[types[j]] * parts for j in range(nseg)]
     total = float(sum(byt))
@@ -48,9 +48,9 @@ def check_shape(rows, types, K, mode, bases):
         return False
     count, J, max_sb, lds = cfg
     S = K // 256
-    parts = 2 if mode == 1 else 1
+    parts = 2 if mode in (1, 3) else 1
     wpp = WAVES // parts
-    nseg = 1 if mode == 1 else len(rows)
+    nseg = 1 if mode in (1, 3) else len(rows)
     seen = [np.zeros((parts, rows[j] * S), np.int64) for j in range(nseg)]
     wave = np.arange(WAVES)[:, None, None]
     lane = np.arange(64)[None, :, None]
@@ -67,7 +67,7 @@ def check_shape(rows, types, K, mode, bases):
             assert nsb <= max_sb
             part, wv = wave // wpp, wave % wpp
             sb_a, sb_b = nsb * wv // wpp, nsb * (wv + 1) // wpp
-            base = np.where(part == 1, bases[1] if mode == 1 else 0, bases[j])
+            base = np.where(part == 1, bases[1] if mode in (1, 3) else 0, bases[j])
             run = base + r0 * rb + np.where(sb_b > sb_a, sb_a, 0) * B
             o = run & 3
             if types[j] == 12:
@@ -100,6 +100,15 @@ def check_shape(rows, types, K, mode, bases):
     for j in range(nseg):
         assert np.all(seen[j] == 1), "every superblock of every row exactly once"
     assert lds <= MAX_LDS
+    if mode == 3:
+        # the norm scale is staged like x: task t reads scale[8t, 8t+8), t
+        # clamped to the last task; the wave partials of the sum of squares
+        # take the first WAVES floats of the weight staging area
+        groups = K // 8
+        nq = min(WAVES, -(-groups // (64 * XSTAGED)))
+        t = np.minimum(np.arange(64 * nq)[:, None] + 64 * nq * np.arange(XSTAGED)[None, :], groups - 1)
+        assert t.min() >= 0 and 8 * t.max() + 8 <= K
+        assert 4 * WAVES <= WAVES * J * 1024
     return True
 
 
@@ -117,6 +126,9 @@ SHAPES = [
     ([1000], [14], 2560, 0),
     ([64], [14], 9728, 0),
     ([5, 5], [14, 14], 2560, 1),
+    ([9728, 9728], [12, 12], 2560, 3),   # ffn_norm + gate + up
+    ([5, 5], [12, 12], 256, 3),
+    ([300, 300], [14, 14], 9728, 3),
     ([257], [14], 768, 0),
 ]
 
@@ -130,6 +142,12 @@ def test_whole_share_indices_in_bounds(rows, types, K, mode):
 
 def test_lm_head_takes_the_streaming_kernel():
     assert launcher([151936], [14], 2560, 0) is None
+
+
+def test_q6k_gate_up_does_not_fit_the_whole_share_kernel():
+    # 2 x 9728 Q6_K rows of width 2560: the FFN (and its norm fold) goes to
+    # the norm kernel and the streaming kernel instead
+    assert launcher([9728, 9728], [14, 14], 2560, 3) is None
 
 
 # ---- the batched whole-share kernel (gemv_stream_mt.hpp), M = 2..8 ----
