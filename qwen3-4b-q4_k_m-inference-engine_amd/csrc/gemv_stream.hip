@@ -214,8 +214,10 @@ hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t str
   if (J > kStreamMaxJ) return hipSuccess;
   type = q4 && q6 ? 0 : q4 ? QK_TYPE_Q4_K : QK_TYPE_Q6_K;
   sp.max_sb = static_cast<int32_t>(max_sb);
+  // (mode 3: the wave partials of the row's sum of squares after the sums)
   const int64_t lds = S * 8 * static_cast<int64_t>(sizeof(qk_q8_block)) +
-                      static_cast<int64_t>(kStreamWaves) * J * 1024 + parts * max_sb * 4;
+                      static_cast<int64_t>(kStreamWaves) * J * 1024 + parts * max_sb * 4 +
+                      (mode == 3 ? 4 * kStreamWaves : 0);
   if (lds > max_lds) return hipSuccess;
   const StreamKernel fn = stream_kernel(type, J, mode);
   if (!fn) return hipSuccess;

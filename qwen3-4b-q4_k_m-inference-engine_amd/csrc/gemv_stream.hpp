@@ -116,11 +116,12 @@ struct WaveShare {
 // chunk moved back at the matrix end can sit off a 16-byte boundary.
 // IL: each round right after the chunks it needs (measured faster for the
 // mixed-type q/k/v launch); otherwise every chunk first, then the rounds.
+// Row totals are multiplied by out_scale (1 outside the RMSNorm fold).
 template <int TYPE, int J, int MODE, bool IL>
 __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, int max_sb, int r0,
                                                int r1, global_f32* yout, global_f32* hout,
                                                const lds_q8_block* xq, lds_u8* wlds,
-                                               lds_f32* sums) {
+                                               lds_f32* sums, float out_scale) {
   constexpr int B = TYPE == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes;
   const int lane = static_cast<int>(threadIdx.x & 63u);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -188,8 +189,8 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
       g += sums[i * S + t];
       if constexpr (MODE == 1) u += sums[max_sb + i * S + t];
     }
-    g = add_dpp<0x4E>(add_dpp<0xB1>(g));
-    if constexpr (MODE == 1) u = add_dpp<0x4E>(add_dpp<0xB1>(u));
+    g = add_dpp<0x4E>(add_dpp<0xB1>(g)) * out_scale;
+    if constexpr (MODE == 1) u = add_dpp<0x4E>(add_dpp<0xB1>(u)) * out_scale;
     if (k == 0) {
       if constexpr (MODE == 0) yout[r0 + i] = g;
       else hout[r0 + i] = (g / (1.0f + expf(-g))) * u;
@@ -203,10 +204,15 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
 // the same straight-line code and the quantiser's waits count them exactly;
 // only the consumption is specialised per type.
 // MODE 0: y_j = x . W_j^T per segment; 1: h = SiLU(x . gate^T) * (x . up^T);
-// 3: mode 1 on RMSNorm(x) (src/cuda/rms_norm.cu:6-24 folded into the
-// prologue: the quantiser waves also stage the norm scale, take the row's
-// sum of squares once the weight loads are out, and quantise
-// (x * rsqrt(mean(x^2) + eps)) * scale).
+// 3: mode 1 on RMSNorm(x) = (x * inv) * scale, inv = rsqrt(mean(x^2) + eps)
+// (src/cuda/rms_norm.cu:6-24 folded into the launch). The Q8 round trip is
+// scale-invariant (codes = round(127 v / amax), block scale amax / 127), so
+// the quantiser waves quantise x * scale as soon as their activations arrive,
+// with no wait for the row's sum of squares, and the gate and up row totals
+// are multiplied by inv instead; the sum's wave partials go to LDS before the
+// activation barrier. Against quantising the normalised row this moves
+// only fp32 rounding (a code can step at a near-tie), while |x * scale| stays
+// in fp32's normal range.
 template <int TYPE, int J, int MODE>
 __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const StreamParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -290,13 +296,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   lds_q8_block* xq = (lds_q8_block*)(lds_raw);
   lds_u8* wlds = (lds_u8*)(lds_raw) + S * 8 * static_cast<int>(sizeof(qk_q8_block));
   lds_f32* sums = reinterpret_cast<lds_f32*>(wlds + kStreamWaves * J * 1024);
+  // MODE 3: the quantiser waves' partial sums of squares, after the
+  // superblock sums of both parts
+  lds_f32* norm_part = sums + 2 * max_sb;
   if constexpr (MODE == 3) {
-    // the row's sum of squares: lanes, then waves in order (one barrier);
-    // the wave partials sit in the weight staging area, unused until the
-    // consume loop, which starts after the next barrier
-    lds_f32* norm_part = reinterpret_cast<lds_f32*>(wlds);
-    float ss = 0.0f;
     if (wave < nq) {
+      float ss = 0.0f;
 #pragma unroll
       for (int i = 0; i < kXStaged; ++i) {
         const int t = static_cast<int>(threadIdx.x) + 64 * nq * i;
@@ -304,37 +309,33 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
         if (t < K / 8)
           ss += ((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w)) +
                 ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
+        stage.a[i] = a * nstage.a[i];
+        stage.b[i] = b * nstage.b[i];
       }
-    }
-    ss = row_lanes_sum<64>(ss);  // DPP and lane swaps: no LDS round trips
-    if (lane == 0) norm_part[wave] = ss;
-    __syncthreads();
-    float total = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kStreamWaves; ++i) total += norm_part[i];
-    const float inv = rsqrtf(total / static_cast<float>(K) + eps);
-    if (wave < nq) {
-#pragma unroll
-      for (int i = 0; i < kXStaged; ++i) {
-        stage.a[i] = (stage.a[i] * inv) * nstage.a[i];
-        stage.b[i] = (stage.b[i] * inv) * nstage.b[i];
-      }
+      ss = row_lanes_sum<64>(ss);  // DPP and lane swaps: no LDS round trips
+      if (lane == 0) norm_part[wave] = ss;
     }
   }
   if (wave < nq) quantize_staged_into_lds<1>(1, K, nq, stage, xq);  // K <= kStreamMaxK: all staged
   __syncthreads();
+  float out_scale = 1.0f;
+  if constexpr (MODE == 3) {
+    float total = 0.0f;  // the waves' partials in wave order
+    for (int i = 0; i < nq; ++i) total += norm_part[i];
+    out_scale = rsqrtf(total / static_cast<float>(K) + eps);
+  }
 
   // outputs in the global address space (the register copies above lost it)
   global_f32* gy = (global_f32*)(yout);
   global_f32* gh = (global_f32*)(hout);
 
   if constexpr (TYPE != 0) {
-    stream_consume<TYPE, J, kFfn ? 1 : MODE, false>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums);
+    stream_consume<TYPE, J, kFfn ? 1 : MODE, false>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums, out_scale);
   } else {
     if (type == QK_TYPE_Q4_K)
-      stream_consume<QK_TYPE_Q4_K, J, kFfn ? 1 : MODE, true>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums);
+      stream_consume<QK_TYPE_Q4_K, J, kFfn ? 1 : MODE, true>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums, out_scale);
     else
-      stream_consume<QK_TYPE_Q6_K, J, kFfn ? 1 : MODE, true>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums);
+      stream_consume<QK_TYPE_Q6_K, J, kFfn ? 1 : MODE, true>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums, out_scale);
   }
 }
 

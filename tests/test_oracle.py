@@ -346,3 +346,25 @@ def test_rms_norm_oracle(oracle):
     tiny = np.full(width, 1e-4, np.float32)
     out = oracle.rms_norm(tiny, ones, width, 1.0)  # mean 1e-8 << eps = 1
     assert np.allclose(out, 1e-4 / np.sqrt(1.0 + 1e-8), rtol=1e-6)
+
+
+def test_q8_scale_invariance_behind_the_norm_fold(oracle):
+    """The fused FFN's RMSNorm fold quantises x * scale and multiplies the row
+    totals by inv_rms: it relies on Q8(c * v) = (codes(v), c * scales(v)).
+    For c a power of two this holds bit for bit; for a general c > 0 codes
+    may step only where 127 * v / amax sits within rounding of a half."""
+    rng = np.random.default_rng(11)
+    v = (rng.standard_normal(32 * 512) * np.exp(rng.uniform(-8, 8, 32 * 512))).astype(np.float32)
+    codes, scales = oracle.quantize_q8(v)
+    for c in (2.0 ** -20, 0.5, 8.0, 2.0 ** 30):
+        c_codes, c_scales = oracle.quantize_q8(v * np.float32(c))
+        assert np.array_equal(c_codes, codes)
+        assert np.array_equal(c_scales, (scales * np.float32(c)).astype(np.float32))
+    c = np.float32(0.037)
+    c_codes, c_scales = oracle.quantize_q8(v * c)
+    assert np.allclose(c_scales, scales * c, rtol=2e-7, atol=0)
+    t = 127.0 * v.astype(np.float64) / np.repeat(scales.astype(np.float64) * 127.0, 32)
+    moved = c_codes != codes
+    assert np.all(np.abs(c_codes[moved].astype(int) - codes[moved]) == 1)
+    assert np.all(np.abs(np.abs(t[moved] - np.floor(t[moved])) - 0.5) < 1e-4)
+    assert moved.mean() < 1e-3

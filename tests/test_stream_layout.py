@@ -36,7 +36,7 @@ def launcher(rows, types, K, mode):
         max_sb = max(max_sb, sb)
     if J > MAX_J:
         return None
-    lds = S * 8 * 48 + WAVES * J * 1024 + parts * max_sb * 4
+    lds = S * 8 * 48 + WAVES * J * 1024 + parts * max_sb * 4 + (4 * WAVES if mode == 3 else 0)
     if lds > MAX_LDS:
         return None
     return count, J, max_sb, lds
@@ -102,13 +102,14 @@ def check_shape(rows, types, K, mode, bases):
     assert lds <= MAX_LDS
     if mode == 3:
         # the norm scale is staged like x: task t reads scale[8t, 8t+8), t
-        # clamped to the last task; the wave partials of the sum of squares
-        # take the first WAVES floats of the weight staging area
+        # clamped to the last task; the quantiser waves' partial sums of
+        # squares follow the superblock sums of both parts
         groups = K // 8
         nq = min(WAVES, -(-groups // (64 * XSTAGED)))
         t = np.minimum(np.arange(64 * nq)[:, None] + 64 * nq * np.arange(XSTAGED)[None, :], groups - 1)
         assert t.min() >= 0 and 8 * t.max() + 8 <= K
-        assert 4 * WAVES <= WAVES * J * 1024
+        norm_part = S * 8 * 48 + WAVES * J * 1024 + 4 * (2 * max_sb)
+        assert norm_part % 4 == 0 and norm_part + 4 * nq <= lds
     return True
 
 
