@@ -47,11 +47,11 @@ struct StreamSegment {
 struct StreamParams {
   const float* x;
   float* h;
-  const float* norm;  // MODE 3: RMSNorm scale [K] applied to x before the Q8 round trip
   int32_t K, S, nseg, max_sb;  // max_sb: superblocks of the largest workgroup share (per part)
-  float eps;                   // MODE 3: RMSNorm epsilon
-  int32_t pad0, pad1, pad2;
   StreamSegment seg[kMaxSegments];
+  const float* norm;  // MODE 3: RMSNorm scale [K]
+  float eps;          // MODE 3: RMSNorm epsilon
+  int32_t pad;
 };
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -116,8 +116,8 @@ struct WaveShare {
 // chunk moved back at the matrix end can sit off a 16-byte boundary.
 // IL: each round right after the chunks it needs (measured faster for the
 // mixed-type q/k/v launch); otherwise every chunk first, then the rounds.
-// Row totals are multiplied by out_scale (1 outside the RMSNorm fold).
-template <int TYPE, int J, int MODE, bool IL>
+// SCALED: row totals are multiplied by out_scale (the RMSNorm fold).
+template <int TYPE, int J, int MODE, bool IL, bool SCALED = false>
 __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, int max_sb, int r0,
                                                int r1, global_f32* yout, global_f32* hout,
                                                const lds_q8_block* xq, lds_u8* wlds,
@@ -189,8 +189,12 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
       g += sums[i * S + t];
       if constexpr (MODE == 1) u += sums[max_sb + i * S + t];
     }
-    g = add_dpp<0x4E>(add_dpp<0xB1>(g)) * out_scale;
-    if constexpr (MODE == 1) u = add_dpp<0x4E>(add_dpp<0xB1>(u)) * out_scale;
+    g = add_dpp<0x4E>(add_dpp<0xB1>(g));
+    if constexpr (MODE == 1) u = add_dpp<0x4E>(add_dpp<0xB1>(u));
+    if constexpr (SCALED) {
+      g *= out_scale;
+      u *= out_scale;
+    }
     if (k == 0) {
       if constexpr (MODE == 0) yout[r0 + i] = g;
       else hout[r0 + i] = (g / (1.0f + expf(-g))) * u;
@@ -224,8 +228,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   for (int j = 0; j < kMaxSegments; ++j)
     asm volatile("" ::"s"(p.seg[j].w), "s"(p.seg[j].y), "s"(p.seg[j].rows), "s"(p.seg[j].type),
                  "s"(p.seg[j].wg_begin), "s"(p.seg[j].per), "s"(p.seg[j].rem), "s"(p.seg[j].pad));
-  asm volatile("" ::"s"(p.x), "s"(p.h), "s"(p.norm), "s"(p.K), "s"(p.S), "s"(p.nseg), "s"(p.max_sb),
-               "s"(p.eps), "s"(p.pad0), "s"(p.pad1), "s"(p.pad2));
+  asm volatile("" ::"s"(p.x), "s"(p.h), "s"(p.K), "s"(p.S), "s"(p.nseg), "s"(p.max_sb));
+  if constexpr (MODE == 3) asm volatile("" ::"s"(p.norm), "s"(p.eps));
   __builtin_amdgcn_sched_barrier(0);
   const int K = p.K, nseg = p.nseg;
 
@@ -259,8 +263,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   // arguments, the compiler re-reads them from memory there (a round trip).
   int S = p.S, max_sb = p.max_sb;
   float* hout = p.h;
-  float eps = p.eps;
-  asm volatile("" : "+s"(S), "+s"(max_sb), "+s"(hout), "+s"(yout), "+s"(r0), "+s"(r1), "+s"(eps));
+  asm volatile("" : "+s"(S), "+s"(max_sb), "+s"(hout), "+s"(yout), "+s"(r0), "+s"(r1));
+  float eps = 0.0f;
+  if constexpr (MODE == 3) {
+    eps = p.eps;
+    asm volatile("" : "+s"(eps));
+  }
 
   // The wave's run [sb_a, sb_b) as 16-byte chunks. An idle wave reads the
   // workgroup's first chunk. The last chunk of the matrix is moved back so it
@@ -330,12 +338,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   global_f32* gh = (global_f32*)(hout);
 
   if constexpr (TYPE != 0) {
-    stream_consume<TYPE, J, kFfn ? 1 : MODE, false>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums, out_scale);
+    stream_consume<TYPE, J, kFfn ? 1 : MODE, false, MODE == 3>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums, out_scale);
   } else {
     if (type == QK_TYPE_Q4_K)
-      stream_consume<QK_TYPE_Q4_K, J, kFfn ? 1 : MODE, true>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums, out_scale);
+      stream_consume<QK_TYPE_Q4_K, J, kFfn ? 1 : MODE, true, MODE == 3>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums, out_scale);
     else
-      stream_consume<QK_TYPE_Q6_K, J, kFfn ? 1 : MODE, true>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums, out_scale);
+      stream_consume<QK_TYPE_Q6_K, J, kFfn ? 1 : MODE, true, MODE == 3>(ws, S, max_sb, r0, r1, gy, gh, xq, wlds, sums, out_scale);
   }
 }
 
