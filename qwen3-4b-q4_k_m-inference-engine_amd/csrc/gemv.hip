@@ -112,7 +112,7 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
   if (e != hipSuccess) return e;
   const int M = p.M;
   const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
-  const int waves = mt == 1 ? (mode == 2 ? matvec_waves<1, 2>() : matvec_waves<1>()) : matvec_waves<8>();
+  const int waves = mt == 1 ? matvec_waves<1>() : matvec_waves<8>();
   const size_t lds = static_cast<size_t>(mt) * static_cast<size_t>(p.K / 32) * sizeof(qk_q8_block);
   if (lds > dev.max_lds) return hipErrorInvalidValue;
 

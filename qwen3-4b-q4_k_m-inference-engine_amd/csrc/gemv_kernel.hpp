@@ -32,12 +32,7 @@ namespace qk {
 
 // Waves per workgroup, iterations per chunk (Q4_K, Q6_K) and activation
 // tasks staged per quantiser lane. The defaults are the values measured best
-// on the Qwen3-4B decode sweep (16 waves of at most 128 VGPRs, shallow
-// chunks: more waves in flight beat deeper per-wave unrolling); the macros
-// exist for tuning builds.
-#ifndef QK_MATVEC_WAVES
-#define QK_MATVEC_WAVES 16
-#endif
+// on the Qwen3-4B decode sweep; the macros exist for tuning builds.
 #ifndef QK_MATVEC_WAVES_MT
 #define QK_MATVEC_WAVES_MT 8  // M > 1: several accumulators per lane need 256 VGPRs
 #endif
@@ -50,22 +45,20 @@ namespace qk {
 #ifndef QK_MATVEC_XSTAGED
 #define QK_MATVEC_XSTAGED 2
 #endif
-// The argmax mode (M = 1, the lm_head: one long stream per wave) is measured
-// faster with half the waves, each two Q6_K iterations deep (196 VGPRs; 16
-// waves that deep spill).
-#ifndef QK_MATVEC_WAVES_ARGMAX
-#define QK_MATVEC_WAVES_ARGMAX 8
+// M = 1 on this kernel means a shape too large for the whole-share kernel
+// (the lm_head: one long stream per wave), measured faster with 8 waves
+// each two Q6_K iterations deep (196 VGPRs; 16 waves that deep spill) than
+// with 16 waves one iteration deep.
+#ifndef QK_MATVEC_WAVES_M1
+#define QK_MATVEC_WAVES_M1 8
 #endif
-#ifndef QK_MATVEC_U4_ARGMAX
-#define QK_MATVEC_U4_ARGMAX 2
+#ifndef QK_MATVEC_U6_M1
+#define QK_MATVEC_U6_M1 2
 #endif
-#ifndef QK_MATVEC_U6_ARGMAX
-#define QK_MATVEC_U6_ARGMAX 2
-#endif
-// Waves per workgroup for MT activation rows (MODE 2: the argmax mode).
-template <int MT, int MODE = 0>
+// Waves per workgroup for MT activation rows.
+template <int MT>
 constexpr int matvec_waves() {
-  return MT == 1 ? (MODE == 2 ? QK_MATVEC_WAVES_ARGMAX : QK_MATVEC_WAVES) : QK_MATVEC_WAVES_MT;
+  return MT == 1 ? QK_MATVEC_WAVES_M1 : QK_MATVEC_WAVES_MT;
 }
 
 // Per-lane register image of one iteration's piece.
@@ -177,9 +170,9 @@ struct XStage {
 };
 
 // Quantiser waves for `tasks` tasks: enough for kXStaged tasks per lane.
-template <int MT, int MODE = 0>
+template <int MT>
 __device__ __forceinline__ int quantiser_waves(int tasks) {
-  return min(matvec_waves<MT, MODE>(), (tasks + 64 * kXStaged - 1) / (64 * kXStaged));
+  return min(matvec_waves<MT>(), (tasks + 64 * kXStaged - 1) / (64 * kXStaged));
 }
 
 // Loads of every staged task are unconditional (indices clamped into the
@@ -246,13 +239,13 @@ __device__ void quantize_into_lds(const float* __restrict__ x, int M, int K, int
 }
 
 // Caller-provided Q8 blocks [M][K/32] -> LDS [MT][K/32]; rows m >= M are zero.
-template <int MT, int MODE>
+template <int MT>
 __device__ void copy_q8_into_lds(const qk_q8_block* __restrict__ q8, int M, int K,
                                  lds_q8_block* lds) {
   const int per_row = (K / 32) * 3;  // 16-byte chunks
   const u32x4* src = reinterpret_cast<const u32x4*>(q8);
   lds_u32x4* dst = reinterpret_cast<lds_u32x4*>(lds);
-  for (int t = threadIdx.x; t < MT * per_row; t += 64 * matvec_waves<MT, MODE>()) {
+  for (int t = threadIdx.x; t < MT * per_row; t += 64 * matvec_waves<MT>()) {
     const int m = t / per_row;
     dst[t] = m < M ? src[t] : u32x4{0u, 0u, 0u, 0u};
   }
@@ -334,7 +327,7 @@ __device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo,
   // g % nworkers, worker = wave*nwg + wg, so consecutive groups run on
   // different CUs and, at any moment, the whole GPU streams one compact
   // window of the matrix (DRAM rows stay open for many requests).
-  const int nworkers = nwg * matvec_waves<MT, MODE>();
+  const int nworkers = nwg * matvec_waves<MT>();
   const int wid = wave * nwg + wg;
   const int groups_total = (row_hi - row_lo + kRPU - 1) / kRPU;
   const int ngroups = wid < groups_total ? (groups_total - 1 - wid) / nworkers + 1 : 0;
@@ -391,7 +384,7 @@ __device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo,
 
   // The first U iterations' weights are requested before the activations are
   // quantised; a quantiser wave's activation loads go out just ahead of them.
-  const int nq = quantiser_waves<MT, MODE>(MT * (K / 8));
+  const int nq = quantiser_waves<MT>(MT * (K / 8));
   const bool quantiser = wave < nq;  // wave-uniform
   XStage<MT> stage;
   Piece fa[U], fb[U];
@@ -402,7 +395,7 @@ __device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo,
   issue(ci, fa);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (Q8IN) {
-    copy_q8_into_lds<MT, MODE>(a.q8, M, K, xq);
+    copy_q8_into_lds<MT>(a.q8, M, K, xq);
   } else {
     if (quantiser) quantize_into_lds<MT>(a.x, M, K, nq, stage, xq);
   }
@@ -508,11 +501,11 @@ __device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo,
 // [0, split_row), the others the Q6_K rows, each with a body specialised to
 // its type. Q8IN: activations arrive as Q8 blocks (q8) instead of fp32 (x).
 template <int MT, int LPR, int MODE, int TYPE, bool Q8IN>
-__global__ __launch_bounds__((64 * matvec_waves<MT, MODE>())) void matvec_kernel(const MatvecParams p) {
+__global__ __launch_bounds__((64 * matvec_waves<MT>())) void matvec_kernel(const MatvecParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   lds_q8_block* xq = (lds_q8_block*)(lds_raw);
-  constexpr int U4 = MODE == 2 ? QK_MATVEC_U4_ARGMAX : QK_MATVEC_U4;
-  constexpr int U6 = MODE == 2 ? QK_MATVEC_U6_ARGMAX : QK_MATVEC_U6;
+  constexpr int U4 = QK_MATVEC_U4;
+  constexpr int U6 = MT == 1 ? QK_MATVEC_U6_M1 : QK_MATVEC_U6;
 
   MatvecArgs a;
   a.x = p.x;
@@ -544,9 +537,9 @@ __global__ __launch_bounds__((64 * matvec_waves<MT, MODE>())) void matvec_kernel
     const uint64_t key = matvec_body<MT, LPR, TYPE == QK_TYPE_Q4_K ? U4 : U6, MODE, TYPE, Q8IN>(
         a, 0, rows_total, wg, grid, xq);
     if constexpr (MODE == 2) {
-      __shared__ uint64_t keys[matvec_waves<MT, MODE>() + 1];
+      __shared__ uint64_t keys[matvec_waves<MT>() + 1];
       argmax_finish(key, static_cast<ArgmaxWorkspace*>(argmax_ws), argmax_result, keys,
-                    matvec_waves<MT, MODE>());
+                    matvec_waves<MT>());
     }
   } else {
     if (wg < split_wg)

@@ -234,7 +234,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   const int K = p.K, nseg = p.nseg;
 
   // The activation loads of the quantiser waves go out first.
-  const int nq = quantiser_waves<1>(K / 8);
+  // (capped by this kernel's own wave count: K <= kStreamMaxK stages every task)
+  const int nq = min(kStreamWaves, (K / 8 + 64 * kXStaged - 1) / (64 * kXStaged));
   const int lane = static_cast<int>(threadIdx.x & 63u);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   XStage<1> stage, nstage;  // nstage: MODE 3's norm scale of the staged tasks
