@@ -368,6 +368,29 @@ def test_ffn_gate_up_norm(gpu, oracle, qtype, M):
     assert oracle.row_norm_error(got, h2.download(np.float32).reshape(M, N).astype(np.float64)) <= 1e-3
 
 
+@pytest.mark.parametrize("qtype,K,N,eps,xscale", [(Q4, 256, 5, 1.0, 0.3), (Q6, 512, 37, 1e-6, 1e-3),
+                                                  (Q4, 4096, 300, 0.5, 2.0)])
+def test_ffn_gate_up_norm_small_shapes(gpu, oracle, qtype, K, N, eps, xscale):
+    """The fold at M = 1 on small shapes, with eps large enough against mean(x^2) that a
+    misplaced eps or a missing 1/K in the mean moves the result far past the bar."""
+    gate = make_weight(gpu, oracle, qtype, N, K, SEED + 720)
+    up = make_weight(gpu, oracle, qtype, N, K, SEED + 721)
+    x = oracle.synth_normal(K, SEED + 722) * np.float32(xscale)
+    scale = (np.float32(1.0) + np.float32(0.3) * oracle.synth_normal(K, SEED + 723)).astype(np.float32)
+    xd, sd = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer.from_array(scale)
+    h = gpu.DeviceBuffer(4 * N)
+    gpu.ffn_gate_up_norm(xd, sd, eps, gate, up, qtype, K, N, h, 1)
+    gpu.synchronize()
+    got = h.download(np.float32).reshape(1, N)
+    n = oracle.rms_norm(x, scale, K, eps)
+    g = oracle.reference_product(n, gate.download(np.uint8), qtype, K, N)
+    u = oracle.reference_product(n, up.download(np.uint8), qtype, K, N)
+    ref = (g / (1.0 + np.exp(-g))) * u
+    err = oracle.row_norm_error(got, ref)
+    print(f"ffn+norm K={K} N={N} eps={eps} row-norm error {err:.3e}")
+    assert err <= 1e-3
+
+
 def test_prologue_quantisation_matches_quantize_kernel(gpu, oracle):
     """The in-kernel Q8 (reciprocal + correction) equals the IEEE-division quantize
     kernel on wide-range data with many exact rounding ties."""

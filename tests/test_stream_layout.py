@@ -129,6 +129,8 @@ SHAPES = [
     ([5, 5], [14, 14], 2560, 1),
     ([9728, 9728], [12, 12], 2560, 3),   # ffn_norm + gate + up
     ([5, 5], [12, 12], 256, 3),
+    ([37, 37], [14, 14], 512, 3),
+    ([300, 300], [12, 12], 4096, 3),
     ([300, 300], [14, 14], 9728, 3),
     ([257], [14], 768, 0),
 ]
