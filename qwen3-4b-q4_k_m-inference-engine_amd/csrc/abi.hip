@@ -141,9 +141,22 @@ int run_gemm(const float* x, int64_t M, int64_t K, const qk_segment* segments, i
     if (error != hipSuccess) return hip_fail(error, "matmul workspace allocation failed");
   }
   hipError_t error = qk::launch_gemm_prep(x, M, K, scratch, stream);
-  for (int j = 0; j < count && error == hipSuccess; ++j)
+  for (int j = 0; j < count && error == hipSuccess; ++j) {
+    if (j + 1 < count && segments[j + 1].type == segments[j].type) {
+      // two matrices of one type in one launch fill more CUs (attn q and k)
+      bool launched = false;
+      error = qk::launch_gemm_core_pair(scratch, segments[j].type, K, M, segments[j].w,
+                                        segments[j].N, segments[j].y, segments[j + 1].w,
+                                        segments[j + 1].N, segments[j + 1].y, stream, launched);
+      if (error != hipSuccess) break;
+      if (launched) {
+        ++j;
+        continue;
+      }
+    }
     error = qk::launch_gemm_core(scratch, segments[j].w, segments[j].type, K, segments[j].N,
                                  segments[j].y, M, stream);
+  }
   if (!workspace) (void)hipFreeAsync(scratch, stream);
   return error == hipSuccess ? QK_OK : hip_fail(error, "matmul launch failed");
 }

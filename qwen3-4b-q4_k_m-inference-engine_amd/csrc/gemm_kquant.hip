@@ -83,6 +83,12 @@ struct KQGemmArgs {
   int32_t M, N, K, S;
   float* part;  // splits > 1: unscaled partial products [splits][M][N]
   int32_t n_tiles, tiles, per_xcd, splits;
+  // A second weight matrix of the same type and K on the same activations
+  // (N1 > 0, one split only): n-tiles from n_tiles0 on are its, written to
+  // y1 [M x N1].
+  const uint8_t* w1;
+  float* y1;
+  int32_t N1, n_tiles0;
 };
 
 // 8 weights (bytes of dwords lo, hi; nibble U) -> fp16 sc*q.
@@ -145,9 +151,19 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArg
   const int u = (b & 7) * args.per_xcd + (b >> 3);
   if ((b >> 3) >= args.per_xcd || u >= args.tiles * args.splits) return;
   const int t = u / args.splits, split = u % args.splits;
-  const int mt = t / args.n_tiles, nt = t % args.n_tiles;
+  const int mt = t / args.n_tiles;
+  int nt = t % args.n_tiles;
+  const uint8_t* wmat = args.w;
+  float* ymat = args.y;
+  int N = args.N;
+  if (args.N1 > 0 && nt >= args.n_tiles0) {  // the second matrix's tiles
+    wmat = args.w1;
+    ymat = args.y1;
+    N = args.N1;
+    nt -= args.n_tiles0;
+  }
   const int m0 = mt * C::BM, n0 = nt * C::BN;
-  const int M = args.M, N = args.N, K = args.K, S = args.S;
+  const int M = args.M, K = args.K, S = args.S;
   const int sb0 = split * S / args.splits, sb1 = (split + 1) * S / args.splits;
   const int c_last = 4 * sb1 - 1;  // loads past the split's end re-read its last stage
 
@@ -177,7 +193,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArg
   const uint8_t* wrow[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j)
-    wrow[j] = args.w +
+    wrow[j] = wmat +
               static_cast<int64_t>(min(n0 + wave * 32 * TN + 32 * j + l32, N - 1)) * S * B;
   const _Float16* xrow[TM];
 #pragma unroll
@@ -435,7 +451,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArg
         const int n = n0 + wave * 32 * TN + 32 * j + l32;
         if (n >= N) continue;
         if (args.splits == 1)
-          args.y[static_cast<int64_t>(m) * N + n] = acc[i][j][r] * rs;
+          ymat[static_cast<int64_t>(m) * N + n] = acc[i][j][r] * rs;
         else
           part[static_cast<int64_t>(m) * N + n] = acc[i][j][r];
       }
@@ -460,7 +476,8 @@ __global__ __launch_bounds__(256) void gemm_kq_reduce_kernel(const float* __rest
 template <int TYPE, int TM, int TN>
 hipError_t launch_cfg(KQGemmArgs a, hipStream_t stream) {
   using C = KQCfg<TM, TN>;
-  a.n_tiles = (a.N + C::BN - 1) / C::BN;
+  a.n_tiles0 = (a.N + C::BN - 1) / C::BN;
+  a.n_tiles = a.n_tiles0 + (a.N1 > 0 ? (a.N1 + C::BN - 1) / C::BN : 0);
   a.tiles = a.n_tiles * ((a.M + C::BM - 1) / C::BM);
   a.per_xcd = (a.tiles * a.splits + 7) / 8;
   hipLaunchKernelGGL((gemm_kq_kernel<TYPE, TM, TN>), dim3(static_cast<uint32_t>(8 * a.per_xcd)),
@@ -537,6 +554,37 @@ hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, 
                           0, stream>>>(partials, row_scale, y, static_cast<int>(M),
                                        static_cast<int>(N), p.splits);
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_kq_pair(int type, const _Float16* hi, const float* row_scale,
+                               const void* xsums, const void* w0, int64_t N0, float* y0,
+                               const void* w1, int64_t N1, float* y1, int64_t K, int64_t M,
+                               hipStream_t stream, bool& launched) {
+  launched = false;
+  // planned as one matrix of N0 + N1 columns; a split K stays per matrix
+  const KQPlan p = plan(type, M, N0 + N1, K);
+  if (p.splits > 1 || !gemm_kq_fits(M, K, N0 + N1)) return hipSuccess;
+  KQGemmArgs a{};
+  a.hi = hi;
+  a.xs = static_cast<const _Float16*>(xsums);
+  a.row_scale = row_scale;
+  a.w = static_cast<const uint8_t*>(w0);
+  a.y = y0;
+  a.w1 = static_cast<const uint8_t*>(w1);
+  a.y1 = y1;
+  a.M = static_cast<int32_t>(M);
+  a.N = static_cast<int32_t>(N0);
+  a.N1 = static_cast<int32_t>(N1);
+  a.K = static_cast<int32_t>(K);
+  a.S = static_cast<int32_t>(K / 256);
+  a.splits = 1;
+  hipError_t e;
+  if (type == QK_TYPE_Q6_K)
+    e = p.wide ? launch_cfg<QK_TYPE_Q6_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q6_K, 1, 1>(a, stream);
+  else
+    e = p.wide ? launch_cfg<QK_TYPE_Q4_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q4_K, 1, 1>(a, stream);
+  launched = e == hipSuccess;
+  return e;
 }
 
 }  // namespace qk

@@ -188,6 +188,32 @@ def test_prefill_entry_points_agree_bitwise(gpu, oracle, qtype):
         gpu.matmul_ws(xd, w, qtype, K, N, yb, M, ws, need - 256)
 
 
+@pytest.mark.parametrize("M,shapes", [
+    (512, [(Q4, 4096), (Q4, 1024), (Q6, 1024)]),   # attn q, k (one launch) and v
+    (77, [(Q6, 333), (Q6, 129), (Q4, 200), (Q4, 64)]),
+])
+def test_prefill_segments_pairs_match_single_launches(gpu, oracle, M, shapes):
+    """qk_matmul_segments at M > 8 runs two same-type matrices in one GEMM
+    launch: every output equals its single-matrix qk_matmul bit for bit, and
+    the oracle within the bar."""
+    K = 2560
+    ws = [make_weight(gpu, q, N, K, SEED + 60 + i) for i, (q, N) in enumerate(shapes)]
+    x = oracle.synth_normal(M * K, SEED + 61)
+    xd = gpu.DeviceBuffer.from_array(x)
+    ys = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes]
+    gpu.matmul_segments(xd, M, K, [(w, q, N, y) for w, (q, N), y in zip(ws, shapes, ys)])
+    singles = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes]
+    for w, (q, N), y in zip(ws, shapes, singles):
+        gpu.matmul(xd, w, q, K, N, y, M)
+    gpu.synchronize()
+    for w, (q, N), y, y1 in zip(ws, shapes, ys, singles):
+        got = y.download(np.float32)
+        assert np.array_equal(got, y1.download(np.float32))
+        if N <= 1024:
+            ref = float64_reference(oracle, x, w.download(np.uint8), q, K, N, M)
+            check(oracle, got.reshape(M, N), ref, f"segments q{q} N={N}")
+
+
 def test_prefill_graph_replay_with_workspace(gpu, oracle):
     """qk_matmul_ws allocates nothing, so a prefill step can be captured; each
     replay, with eager work in between, equals the eager result."""
