@@ -116,9 +116,11 @@ int qk_matmul_q8(const qk_q8_block *q8, const void *w, int type, int64_t K, int6
 int qk_matmul_segments(const float *x, int64_t M, int64_t K, const qk_segment *segments,
                        int count, qk_stream_t stream);
 
-/* h[M x N] = SiLU(Q8(x) . gate^T) * (Q8(x) . up^T) in one launch, gate and up
- * both `type` with K columns and N rows. Replaces matmul(gate), matmul(up),
- * silu_multiply (src/Engine.cpp:98-100, src/cuda/silu_multiply.cu:6-12). */
+/* h[M x N] = SiLU(Q8(x) . gate^T) * (Q8(x) . up^T), gate and up both `type`
+ * with K columns and N rows: one launch for M <= 8; for M > 8 the prefill
+ * GEMM (gate and up in one launch) into stream-ordered scratch, then the
+ * SiLU kernel. Replaces matmul(gate), matmul(up), silu_multiply
+ * (src/Engine.cpp:98-100, src/cuda/silu_multiply.cu:6-12). */
 int qk_ffn_gate_up(const float *x, const void *gate, const void *up, int type, int64_t K,
                    int64_t N, float *h, int64_t M, qk_stream_t stream);
 

@@ -253,6 +253,30 @@ int qk_matmul_segments(const float* x, int64_t M, int64_t K, const qk_segment* s
   return run_matvec(p, M, K, 0, as_stream(stream));
 }
 
+namespace {
+
+// Prefill FFN (M > 8): gate and up through the GEMM (one launch for both
+// where no split K is needed) into stream-ordered scratch, then
+// SiLU(gate) * up into h.
+int run_ffn_gemm(const float* x, const void* gate, const void* up, int type, int64_t K, int64_t N,
+                 float* h, int64_t M, hipStream_t stream) {
+  float* gu = nullptr;
+  hipError_t error = hipMallocAsync(reinterpret_cast<void**>(&gu),
+                                    2 * static_cast<size_t>(M) * static_cast<size_t>(N) * sizeof(float),
+                                    stream);
+  if (error != hipSuccess) return hip_fail(error, "ffn scratch allocation failed");
+  const qk_segment segments[2] = {{gate, type, N, gu}, {up, type, N, gu + M * N}};
+  int status = run_gemm(x, M, K, segments, 2, nullptr, 0, stream);
+  if (status == QK_OK) {
+    error = qk::launch_silu_multiply(gu, gu + M * N, h, M * N, stream);
+    if (error != hipSuccess) status = hip_fail(error, "silu_multiply launch failed");
+  }
+  (void)hipFreeAsync(gu, stream);
+  return status;
+}
+
+}  // namespace
+
 int qk_ffn_gate_up(const float* x, const void* gate, const void* up, int type, int64_t K, int64_t N,
                    float* h, int64_t M, qk_stream_t stream) {
   const int status = validate_matmul(type, K, N, M);
@@ -263,6 +287,7 @@ int qk_ffn_gate_up(const float* x, const void* gate, const void* up, int type, i
     const int status = validate_weight_pointer(w, type);
     if (status != QK_OK) return status;
   }
+  if (M > qk::kGemvMaxRows) return run_ffn_gemm(x, gate, up, type, K, N, h, M, as_stream(stream));
   qk::MatvecParams p = params_for(x, nullptr);
   p.nseg = 2;
   p.h = h;

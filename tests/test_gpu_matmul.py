@@ -305,9 +305,10 @@ def test_matmul_segments_qkv(gpu, oracle, M):
         assert oracle.row_norm_error(single, got.astype(np.float64)) <= 1e-6
 
 
-@pytest.mark.parametrize("qtype,M", [(Q4, 1), (Q4, 5), (Q6, 2)])
+@pytest.mark.parametrize("qtype,M", [(Q4, 1), (Q4, 5), (Q6, 2), (Q4, 64), (Q6, 17)])
 def test_ffn_gate_up_silu(gpu, oracle, qtype, M):
-    """SiLU(gate) * up of src/Engine.cpp:98-100 in one launch."""
+    """SiLU(gate) * up of src/Engine.cpp:98-100 in one launch (M > 8: gate and up
+    through one GEMM launch, then the SiLU kernel)."""
     K, N = 2560, 9728
     gate = make_weight(gpu, oracle, qtype, N, K, SEED + 700)
     up = make_weight(gpu, oracle, qtype, N, K, SEED + 701)
