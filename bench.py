@@ -267,7 +267,32 @@ def prefill_gemm(qk, stream):
                      "frac_of_fp16_mfma_peak": round(flops / (us * 1e6) / PEAK_FP16_TFLOPS, 4)}
         for b in (w, y, ws):
             b.free()
-    x.free()
+    # the fused FFN entry point at M = 512 (gate and up in one GEMM launch,
+    # stream-ordered scratch, SiLU*up), timed eagerly: it allocates per call
+    N = 9728
+    gate, up = (qk.DeviceBuffer(N * qk.row_bytes(Q4, K)) for _ in range(2))
+    qk.synth_superblocks(gate, Q4, N, K, 20261207, 0.01, 0.01)
+    qk.synth_superblocks(up, Q4, N, K, 20261208, 0.01, 0.01)
+    h = qk.DeviceBuffer(4 * M * N)
+    qk.synchronize()
+    for _ in range(2):
+        qk.ffn_gate_up(x, gate, up, Q4, K, N, h, M, stream)
+    stream.synchronize()
+    start, end = qk.Event(), qk.Event()
+    start.record(stream)
+    for _ in range(10):
+        qk.ffn_gate_up(x, gate, up, Q4, K, N, h, M, stream)
+    end.record(stream)
+    end.synchronize()
+    us = 1000.0 * start.elapsed_ms(end) / 10
+    start.destroy()
+    end.destroy()
+    flops = 2 * 2 * M * N * K
+    out["ffn_gate_up_fused"] = {"shape": f"M={M} K={K} 2 x N={N} Q4_K + SiLU*up", "avg_us": round(us, 2),
+                                "TFLOP/s": round(flops / (us * 1e6), 1),
+                                "frac_of_fp16_mfma_peak": round(flops / (us * 1e6) / PEAK_FP16_TFLOPS, 4)}
+    for b in (gate, up, h, x):
+        b.free()
     return out
 
 
