@@ -1,10 +1,13 @@
 #pragma once
-// Host-callable entry points for the Q4_K/Q6_K dequantize-matmul path, with the
-// signatures and semantics of the reference's include/Kernels.hpp:9-79
-// (kernels::matmul and its neighbours on this path). Float activations are
-// row-major device buffers; launches use the null stream unless a stream is
-// given. Errors surface as the reference's exception types. No HIP header is
-// included; calls go through the C-ABI of libqk_hip.so (include/qk_abi.h).
+// Host-callable entry points with the signatures and semantics of the
+// reference's include/Kernels.hpp:9-79, so that Engine.cpp's calls compile
+// against this header. Float activations are row-major device buffers;
+// launches use the null stream unless a stream is given. Errors surface as the
+// reference's exception types. No HIP header is included; calls go through
+// the C-ABI of libqk_hip.so (include/qk_abi.h).
+//
+// libqk_engine.so defines every function here except rope and attention,
+// which stay with the engine (they are not on the dequantize-matmul path).
 #include <cstddef>
 #include <cstdint>
 #include <stdexcept>
@@ -18,6 +21,11 @@ inline constexpr unsigned threads = 256;
 
 // Compute units of the current device (include/Kernels.hpp:15-26).
 int get_sm_count();
+
+// Throws std::runtime_error("HIP kernel launch failed: ...") if the last
+// kernel launch on this thread failed (include/Kernels.hpp:28-32), for kernels
+// the engine launches itself.
+void check_launch();
 
 // Turns a C-ABI status into the reference's exceptions: invalid arguments and
 // unsupported types -> std::invalid_argument (src/cuda/matmul.cu:132-136),
@@ -53,6 +61,13 @@ private:
 // The reference's name for the same class.
 using CudaStream = Stream;
 
+// output = input * rsqrt(mean(input^2) + epsilon) * scale per row; scale is an
+// F32 weight of `width` values (include/Kernels.hpp:54-55,
+// src/cuda/rms_norm.cu:28-36). Throws std::invalid_argument for width 0, a
+// non-positive epsilon or a scale that is not F32 of that width.
+void rms_norm(const float* input, const Weight& scale, float* output,
+    size_t rows, size_t width, float epsilon);
+
 // output[rows x N] = Q8(input)[rows x K] . weight^T, K = weight.dimension[0],
 // N = weight.dimension[1]; output is overwritten (src/cuda/matmul.cu:130-165).
 void matmul(const float* input, const Weight& weight, float* output, size_t rows,
@@ -60,6 +75,19 @@ void matmul(const float* input, const Weight& weight, float* output, size_t rows
 
 void matmul(const float* input, const Weight& weight, float* output, size_t rows,
     const Stream& stream);
+
+// Rotary embedding and attention (include/Kernels.hpp:63-68): declared with
+// the reference's signatures for the engine's call sites; the engine provides
+// their definitions (src/cuda/rope.cu, src/cuda/attention.cu).
+void rope(float* input, size_t tokens, size_t heads, size_t head_dim,
+    size_t position_offset, float frequency_base);
+
+void attention(const float* q, const float* k, const float* v, float* output,
+    size_t tokens, size_t query_heads, size_t kv_heads, size_t head_dim,
+    size_t query_offset = 0);
+
+// state[i] += branch[i] (include/Kernels.hpp:70, src/cuda/residual_add.cu:15-20).
+void residual_add(float* state, const float* branch, size_t count);
 
 // out = gate/(1+exp(-gate)) * up (src/cuda/silu_multiply.cu:19-23).
 void silu_multiply(const float* gate, const float* up, float* output, size_t count);

@@ -22,6 +22,9 @@ enum ggml_type : int32_t {
     GGML_TYPE_Q6_K = 14,
     GGML_TYPE_Q8_K = 15,
     GGML_TYPE_BF16 = 30,
+    // Past every type id above; code such as src/EmbedLookup.cpp uses it as
+    // the "no type" marker.
+    GGML_TYPE_COUNT = 40,
 };
 
 // Bytes per row of `width` weights for the types this library computes on

@@ -61,6 +61,11 @@ typedef struct qk_segment {
 
 /* Message of the last failing call on this thread ("" if none). */
 const char *qk_last_error(void);
+/* The last product kernel launched by a call on this thread, as
+ * "name<template values> grid=G" ("" if none); diagnostics only, valid until
+ * the next call of qk_last_launch on the same thread. No counterpart in the
+ * reference. */
+const char *qk_last_launch(void);
 /* Library version: major*10000 + minor*100 + patch. */
 int qk_version(void);
 
@@ -83,13 +88,16 @@ int qk_version(void);
  * Q4_K as the exact fp16 integers sc*q (hi*B + lo*B per step, d and dmin*m
  * applied once per superblock), Q6_K as sc*q = fp16(sc*q) + an exact
  * remainder in {-1, 0, 1} (hi*B_hi + lo*B_hi + hi*B_lo, d once per
- * superblock). Shapes with M or N above 2^30 return QK_ERR_RUNTIME. */
+ * superblock). K above 2^30 returns QK_ERR_INVALID_ARGUMENT. */
 int qk_matmul(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
               int64_t M, qk_stream_t stream);
 
-/* Workspace bytes qk_matmul_ws needs for this shape: 0 for M <= 8, else
- * M*K*4 + M*4 rounded up to 16, plus M*(K/256)*32, rounded up to 256 (0 for
- * shapes qk_matmul rejects). */
+/* Workspace bytes qk_matmul_ws needs for this shape (0 for M <= 8 and for
+ * shapes qk_matmul rejects). For M > 8 it holds the activation planes
+ * (M*K*4 + M*4 bytes, rounded up to 16), their block sums (M*(K/256)*32) and,
+ * when the launch plan splits K (few output tiles, deep K), the partial
+ * products (splits*M*N*4); the total is rounded up to 256. The split plan is
+ * internal: size workspaces with this function, not from the formula. */
 size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M);
 
 /* qk_matmul with a caller-owned device workspace (16-byte aligned) of at least
@@ -165,6 +173,24 @@ int qk_matmul_argmax(const float *x, const void *w, int type, int64_t K, int64_t
 int qk_dequantize_rows(const void *packed, float *out, int64_t rows, int64_t K,
                        size_t row_bytes, int type, qk_stream_t stream);
 
+/* out[rows x width] = (x * rsqrt(mean(x^2) + eps)) * scale per row, scale a
+ * device float[width]. Replaces kernels::rms_norm (include/Kernels.hpp:54-55,
+ * src/cuda/rms_norm.cu:6-36): rows == 0 returns QK_OK; width <= 0 (or above
+ * 2^31-1), eps <= 0 or rows above 2^32-1 give QK_ERR_INVALID_ARGUMENT. */
+int qk_rms_norm(const float *x, const float *scale, float *out, int64_t rows, int64_t width,
+                float eps, qk_stream_t stream);
+
+/* state[i] += branch[i] for i < count. Replaces kernels::residual_add
+ * (include/Kernels.hpp:70, src/cuda/residual_add.cu:6-20); count == 0
+ * returns QK_OK. */
+int qk_residual_add(float *state, const float *branch, int64_t count, qk_stream_t stream);
+
+/* Status of the last kernel launch on this thread (the HIP runtime's last
+ * error, which this call clears): QK_OK or QK_ERR_RUNTIME with the message in
+ * qk_last_error(). Replaces the CUDA query of kernels::detail::check_launch
+ * (include/Kernels.hpp:28-32) for engine kernels built outside this library. */
+int qk_check_launch(void);
+
 /* out = gate/(1+exp(-gate)) * up, elementwise. Replaces kernels::silu_multiply
  * (include/Kernels.hpp:72, src/cuda/silu_multiply.cu:19-23). */
 int qk_silu_multiply(const float *gate, const float *up, float *out, int64_t count,
@@ -202,8 +228,12 @@ int qk_event_elapsed_ms(float *ms, qk_event_t start, qk_event_t end);
 
 /* ---------------------------------------------------------------------------
  * Graph capture of a launch sequence on a non-null stream, replayed with one
- * call (the reference lists CUDA Graphs as future work, README.md:42). Every
- * compute entry point may be captured: none allocates or records a memset.
+ * call (the reference lists CUDA Graphs as future work, README.md:42). No
+ * compute entry point records a memset. At M <= 8 none allocates, except
+ * qk_ffn_gate_up_norm outside its M = 1 fold; at M > 8 qk_matmul,
+ * qk_matmul_segments, qk_ffn_gate_up and qk_ffn_gate_up_norm allocate their
+ * scratch stream-ordered (captured as allocation nodes), while the _ws entry
+ * points take a caller workspace and allocate nothing.
  * ------------------------------------------------------------------------- */
 int qk_stream_begin_capture(qk_stream_t stream);
 /* Ends the capture and instantiates it; *graph owns the executable graph. */

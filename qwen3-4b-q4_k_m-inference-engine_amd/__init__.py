@@ -55,6 +55,7 @@ class Segment(ctypes.Structure):
 # name -> argument types (every function returns int status unless listed in _RESTYPES)
 _SIGNATURES = {
     "qk_last_error": [],
+    "qk_last_launch": [],
     "qk_version": [],
     "qk_matmul": [_c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _i64, _c_void_p],
     "qk_matmul_workspace_size": [_int, _i64, _i64, _i64],
@@ -73,6 +74,9 @@ _SIGNATURES = {
                          _size, _c_void_p],
     "qk_dequantize_rows": [_c_void_p, _c_void_p, _i64, _i64, _size, _int, _c_void_p],
     "qk_silu_multiply": [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
+    "qk_rms_norm": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _float, _c_void_p],
+    "qk_residual_add": [_c_void_p, _c_void_p, _i64, _c_void_p],
+    "qk_check_launch": [],
     "qk_malloc": [ctypes.POINTER(_c_void_p), _size],
     "qk_free": [_c_void_p],
     "qk_malloc_async": [ctypes.POINTER(_c_void_p), _size, _c_void_p],
@@ -101,7 +105,8 @@ _SIGNATURES = {
     "qk_synth_superblocks": [_c_void_p, _int, _i64, _i64, _u64, _float, _float, _c_void_p],
     "qk_synth_normal": [_c_void_p, _i64, _u64, _c_void_p],
 }
-_RESTYPES = {"qk_last_error": ctypes.c_char_p, "qk_matmul_workspace_size": _size,
+_RESTYPES = {"qk_last_error": ctypes.c_char_p, "qk_last_launch": ctypes.c_char_p,
+             "qk_matmul_workspace_size": _size,
              "qk_argmax_workspace_size": _size}
 
 _LIB = None
@@ -152,6 +157,12 @@ def check(status: int) -> None:
     if status != QK_OK:
         msg = load().qk_last_error()
         raise QKError(status, msg.decode() if msg else "")
+
+
+def last_launch() -> str:
+    """The last product kernel launched on this thread ("name<values> grid=G")."""
+    text = load().qk_last_launch()
+    return text.decode() if text else ""
 
 
 def row_bytes(qtype: int, K: int) -> int:
@@ -387,6 +398,16 @@ def dequantize_rows(packed, out, rows: int, K: int, row_stride: int, qtype: int,
 
 def silu_multiply(gate, up, out, count: int, stream=None) -> None:
     check(load().qk_silu_multiply(_ptr(gate), _ptr(up), _ptr(out), count, _stream_ptr(stream)))
+
+
+def rms_norm(x, scale, out, rows: int, width: int, eps: float, stream=None) -> None:
+    """qk_rms_norm: out = x * rsqrt(mean(x^2) + eps) * scale, row by row."""
+    check(load().qk_rms_norm(_ptr(x), _ptr(scale), _ptr(out), rows, width, eps, _stream_ptr(stream)))
+
+
+def residual_add(state, branch, count: int, stream=None) -> None:
+    """qk_residual_add: state += branch."""
+    check(load().qk_residual_add(_ptr(state), _ptr(branch), count, _stream_ptr(stream)))
 
 
 def synth_superblocks(w, qtype: int, N: int, K: int, seed: int, dmax: float,

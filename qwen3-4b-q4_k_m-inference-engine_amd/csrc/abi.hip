@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <string>
 #include <cstdint>
+#include <climits>
 
 #include "qk_abi.h"
 #include "qk_launch.hpp"
@@ -17,6 +18,15 @@
 namespace {
 
 thread_local std::string g_last_error;
+
+struct LaunchNote {
+  const char* kernel = nullptr;
+  int nvalues = 0;
+  int values[6] = {0};
+  int64_t grid = 0;
+};
+thread_local LaunchNote g_launch;
+thread_local std::string g_launch_text;
 
 int fail(int code, const std::string& message) {
   g_last_error = message;
@@ -34,13 +44,18 @@ size_t superblock_bytes(int type) {
   return type == QK_TYPE_Q4_K ? 144u : type == QK_TYPE_Q6_K ? 210u : 0u;
 }
 
+// The kernels index a row's activations and superblocks in 32 bits.
+constexpr int64_t kMaxK = int64_t{1} << 30;
+
 // src/cuda/matmul.cu:132-137 (type, K > 0, K % 256 == 0, N > 0), plus the
-// launch-grid bound on rows the reference shares (grid.y = rows).
+// launch-grid bound on rows the reference shares (grid.y = rows) and the
+// kernels' 32-bit width bound.
 int validate_matmul(int type, int64_t K, int64_t N, int64_t M) {
   if (!supported_type(type))
     return fail(QK_ERR_UNSUPPORTED_TYPE, "matmul supports Q4_K and Q6_K weights only");
   if (K <= 0 || K % 256 != 0 || N <= 0 || N > (int64_t{1} << 31) - 64)
     return fail(QK_ERR_INVALID_ARGUMENT, "Invalid matmul weight dimensions");
+  if (K > kMaxK) return fail(QK_ERR_INVALID_ARGUMENT, "Invalid matmul weight dimensions: K exceeds 2^30");
   if (M < 0) return fail(QK_ERR_INVALID_ARGUMENT, "matmul rows must be >= 0");
   return QK_OK;
 }
@@ -169,14 +184,40 @@ int run_gemm_single(const float* x, const void* w, int type, int64_t K, int64_t 
 
 }  // namespace
 
+namespace qk {
+
+void note_launch(const char* kernel, int nvalues, const int* values, int64_t grid) {
+  g_launch.kernel = kernel;
+  g_launch.nvalues = std::min(nvalues, 6);
+  for (int i = 0; i < g_launch.nvalues; ++i) g_launch.values[i] = values[i];
+  g_launch.grid = grid;
+}
+
+}  // namespace qk
+
 extern "C" {
 
 const char* qk_last_error(void) { return g_last_error.c_str(); }
 
+const char* qk_last_launch(void) {
+  if (!g_launch.kernel) return "";
+  std::string text = g_launch.kernel;
+  text += '<';
+  for (int i = 0; i < g_launch.nvalues; ++i) {
+    if (i) text += ',';
+    text += std::to_string(g_launch.values[i]);
+  }
+  text += "> grid=" + std::to_string(g_launch.grid);
+  g_launch_text = text;
+  return g_launch_text.c_str();
+}
+
 int qk_version(void) { return 200; }
 
 size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M) {
-  if (!supported_type(type) || K <= 0 || K % 256 != 0 || N <= 0 || M <= qk::kGemvMaxRows) return 0;
+  if (!supported_type(type) || K <= 0 || K % 256 != 0 || K > kMaxK || N <= 0 ||
+      M <= qk::kGemvMaxRows)
+    return 0;
   return qk::gemm_workspace_bytes(M, K, type, N);
 }
 
@@ -229,6 +270,7 @@ int qk_matmul_segments(const float* x, int64_t M, int64_t K, const qk_segment* s
   if (count < 1 || count > qk::kMaxSegments || !segments)
     return fail(QK_ERR_INVALID_ARGUMENT, "segment count must be in [1, 4]");
   if (K <= 0 || K % 256 != 0) return fail(QK_ERR_INVALID_ARGUMENT, "Invalid matmul weight dimensions");
+  if (K > kMaxK) return fail(QK_ERR_INVALID_ARGUMENT, "Invalid matmul weight dimensions: K exceeds 2^30");
   if (M < 0) return fail(QK_ERR_INVALID_ARGUMENT, "matmul rows must be >= 0");
   for (int j = 0; j < count; ++j) {
     const int status = validate_segment(segments[j]);
@@ -381,6 +423,31 @@ int qk_dequantize_rows(const void* packed, float* out, int64_t rows, int64_t K, 
   const hipError_t error =
       qk::launch_dequantize_rows(packed, out, rows, K, row_bytes, type, as_stream(stream));
   return error == hipSuccess ? QK_OK : hip_fail(error, "dequantize launch failed");
+}
+
+int qk_rms_norm(const float* x, const float* scale, float* out, int64_t rows, int64_t width,
+                float eps, qk_stream_t stream) {
+  if (rows < 0) return fail(QK_ERR_INVALID_ARGUMENT, "RMSNorm rows must be >= 0");
+  if (rows == 0) return QK_OK;  // src/cuda/rms_norm.cu:31
+  if (width <= 0 || width > INT32_MAX || !(eps > 0.0f) || rows > UINT32_MAX)  // :32-34
+    return fail(QK_ERR_INVALID_ARGUMENT,
+                "RMSNorm requires an F32 scale matching the row width and positive epsilon");
+  if (!x || !scale || !out) return fail(QK_ERR_INVALID_ARGUMENT, "RMSNorm pointers must be non-null");
+  const hipError_t error = qk::launch_rms_norm(x, scale, out, rows, width, eps, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "RMSNorm launch failed");
+}
+
+int qk_residual_add(float* state, const float* branch, int64_t count, qk_stream_t stream) {
+  if (count < 0) return fail(QK_ERR_INVALID_ARGUMENT, "count must be >= 0");
+  if (count == 0) return QK_OK;  // src/cuda/residual_add.cu:16
+  if (!state || !branch) return fail(QK_ERR_INVALID_ARGUMENT, "pointers must be non-null");
+  const hipError_t error = qk::launch_residual_add(state, branch, count, as_stream(stream));
+  return error == hipSuccess ? QK_OK : hip_fail(error, "residual_add launch failed");
+}
+
+int qk_check_launch(void) {
+  const hipError_t error = hipGetLastError();
+  return error == hipSuccess ? QK_OK : fail(QK_ERR_RUNTIME, hipGetErrorString(error));
 }
 
 int qk_silu_multiply(const float* gate, const float* up, float* out, int64_t count,

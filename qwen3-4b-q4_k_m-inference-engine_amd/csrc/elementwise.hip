@@ -1,6 +1,6 @@
 // out = gate/(1+exp(-gate)) * up (src/cuda/silu_multiply.cu:6-12), with the
-// ROCm device library's expf; and the row-wise RMSNorm
-// (src/cuda/rms_norm.cu:6-24) with its rsqrtf.
+// ROCm device library's expf; the row-wise RMSNorm (src/cuda/rms_norm.cu:6-24)
+// with its rsqrtf; and state += branch (src/cuda/residual_add.cu:6-9).
 #include "qk_device.hpp"
 #include "qk_launch.hpp"
 
@@ -38,7 +38,23 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
   for (int i = tid; i < width; i += 256) o[i] = (xr[i] * inv) * scale[i];
 }
 
+__global__ __launch_bounds__(256) void residual_add_kernel(float* __restrict__ state,
+                                                           const float* __restrict__ branch,
+                                                           int64_t count) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < count; i += stride)
+    state[i] += branch[i];
+}
+
 }  // namespace
+
+hipError_t launch_residual_add(float* state, const float* branch, int64_t count,
+                               hipStream_t stream) {
+  const int64_t blocks = (count + 255) / 256;
+  const uint32_t grid = static_cast<uint32_t>(blocks < 16384 ? blocks : 16384);
+  residual_add_kernel<<<grid, 256, 0, stream>>>(state, branch, count);
+  return hipGetLastError();
+}
 
 hipError_t launch_rms_norm(const float* x, const float* scale, float* out, int64_t rows,
                            int64_t width, float eps, hipStream_t stream) {

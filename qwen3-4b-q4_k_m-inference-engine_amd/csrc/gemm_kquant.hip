@@ -480,6 +480,7 @@ hipError_t launch_cfg(KQGemmArgs a, hipStream_t stream) {
   a.n_tiles = a.n_tiles0 + (a.N1 > 0 ? (a.N1 + C::BN - 1) / C::BN : 0);
   a.tiles = a.n_tiles * ((a.M + C::BM - 1) / C::BM);
   a.per_xcd = (a.tiles * a.splits + 7) / 8;
+  note("gemm_kq_kernel", 8 * a.per_xcd, TYPE, TM, TN, a.splits);
   hipLaunchKernelGGL((gemm_kq_kernel<TYPE, TM, TN>), dim3(static_cast<uint32_t>(8 * a.per_xcd)),
                      dim3(64 * kWaves), 0, stream, a);
   return hipGetLastError();

@@ -173,6 +173,7 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
   if (!fn) return hipErrorInvalidValue;
   e = blocks_per_cu(fn, 64 * waves, lds, per_cu);  // sets the kernel's dynamic LDS limit
   if (e != hipSuccess) return e;
+  note("matvec_kernel", grid, mt, lpr, mode, type, p.x == nullptr);
   hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(grid)), dim3(64 * waves), lds, stream, p);
   return hipGetLastError();
 }

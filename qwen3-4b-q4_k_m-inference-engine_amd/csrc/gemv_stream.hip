@@ -162,6 +162,7 @@ hipError_t launch_stream_mt(const MatvecParams& p, int mode, hipStream_t stream,
   if (!fn) return hipSuccess;
   e = allow_lds(reinterpret_cast<const void*>(fn), static_cast<int>(lds));
   if (e != hipSuccess) return e;
+  note("stream_mt_kernel", begin, MT, type, J, mode);
   hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(begin)), dim3(64 * kStreamWaves),
                      static_cast<size_t>(lds), stream, sp);
   launched = true;
@@ -223,6 +224,7 @@ hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t str
   if (!fn) return hipSuccess;
   e = allow_lds(reinterpret_cast<const void*>(fn), static_cast<int>(lds));
   if (e != hipSuccess) return e;
+  note("stream_matvec_kernel", begin, type, J, mode);
   hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(begin)), dim3(64 * kStreamWaves),
                      static_cast<size_t>(lds), stream, sp);
   launched = true;

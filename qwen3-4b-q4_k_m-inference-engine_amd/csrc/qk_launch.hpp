@@ -13,6 +13,16 @@ namespace qk {
 
 constexpr int kMaxSegments = 4;
 
+// Records the last product kernel a launcher enqueued on this thread: its
+// name, up to 6 template values and the grid (qk_last_launch formats it;
+// tests and the bench print it to show which instantiation ran).
+void note_launch(const char* kernel, int nvalues, const int* values, int64_t grid);
+template <typename... T>
+inline void note(const char* kernel, int64_t grid, T... values) {
+  const int v[] = {static_cast<int>(values)..., 0};
+  note_launch(kernel, static_cast<int>(sizeof...(T)), v, grid);
+}
+
 // One weight matrix of a mat-vec launch (rows = N, y is [M x N]).
 struct MatvecSegment {
   const uint8_t* w;
@@ -109,6 +119,10 @@ hipError_t launch_dequantize_rows(const void* packed, float* out, int64_t rows, 
 // out[rows x width] = RMSNorm of x with per-column scale (src/cuda/rms_norm.cu:6-24).
 hipError_t launch_rms_norm(const float* x, const float* scale, float* out, int64_t rows,
                            int64_t width, float eps, hipStream_t stream);
+
+// state[i] += branch[i] for i < count (src/cuda/residual_add.cu:6-9).
+hipError_t launch_residual_add(float* state, const float* branch, int64_t count,
+                               hipStream_t stream);
 
 hipError_t launch_silu_multiply(const float* gate, const float* up, float* out, int64_t count,
                                 hipStream_t stream);

@@ -36,6 +36,7 @@ TypeTraits traits(ggml_type type) {
     case GGML_TYPE_Q5_K: return {256, 176};
     case GGML_TYPE_Q6_K: return {256, 210};
     case GGML_TYPE_Q8_K: return {256, 292};
+    case GGML_TYPE_COUNT: break;
     }
     throw std::runtime_error("Unsupported GGUF tensor type " + std::to_string(int(type)));
 }
@@ -128,12 +129,25 @@ GGUF::MetadataValue read_array_value(Reader& in, gguf_type type, uint64_t count)
 
 }  // namespace
 
+// Bytes of a tensor of `type` with ggml dimensions ne (each >= 1). Every
+// product is checked: a corrupt header whose element count or byte size
+// exceeds INT64_MAX is rejected rather than wrapped to a small size that
+// would pass the bounds checks.
 std::size_t gguf_tensor_bytes(ggml_type type, const std::array<int64_t, GGUF_MAX_DIMS>& ne) {
     const TypeTraits t = traits(type);
+    for (int i = 0; i < GGUF_MAX_DIMS; ++i)
+        if (ne[i] <= 0) throw std::runtime_error("GGUF tensor dimension must be positive");
     if (ne[0] % t.block != 0) throw std::runtime_error("GGUF row width is not a whole number of blocks");
-    std::size_t rows = 1;
-    for (int i = 1; i < GGUF_MAX_DIMS; ++i) rows *= static_cast<std::size_t>(ne[i]);
-    return static_cast<std::size_t>(ne[0] / t.block * t.bytes) * rows;
+    int64_t elements = ne[0], bytes = 0;
+    for (int i = 1; i < GGUF_MAX_DIMS; ++i)
+        if (__builtin_mul_overflow(elements, ne[i], &elements))
+            throw std::runtime_error("GGUF tensor element count overflows");
+    int64_t rows = 1;
+    for (int i = 1; i < GGUF_MAX_DIMS; ++i) rows *= ne[i];  // <= elements: no overflow
+    if (__builtin_mul_overflow(ne[0] / t.block * t.bytes, rows, &bytes) ||
+        static_cast<uint64_t>(bytes) > std::numeric_limits<std::size_t>::max())
+        throw std::runtime_error("GGUF tensor byte size overflows");
+    return static_cast<std::size_t>(bytes);
 }
 
 GGUF::GGUF(const std::filesystem::path& path, bool load_weights) : path_(path) {
@@ -183,15 +197,22 @@ GGUF::GGUF(const std::filesystem::path& path, bool load_weights) : path_(path) {
         tensors_.push_back(std::move(info));
     }
     data_offset_ = (in.pos() + alignment_ - 1) / alignment_ * alignment_;
+    // A file with tensors must hold its whole data section; one without may
+    // end before the padding.
+    if (!tensors_.empty() && data_offset_ > in.size())
+        throw std::runtime_error("Incomplete GGUF data section");
     for (size_t i = 0; i < tensors_.size(); ++i) {
-        tensors_[i].file_offset = data_offset_ + offsets[i];
-        if (tensors_[i].file_offset > in.size() || tensors_[i].bytes > in.size() - tensors_[i].file_offset)
+        if (offsets[i] % alignment_ != 0)
+            throw std::runtime_error("GGUF tensor data is not aligned: " + tensors_[i].name);
+        if (offsets[i] > in.size() - data_offset_ ||
+            tensors_[i].bytes > in.size() - data_offset_ - offsets[i])
             throw std::runtime_error("Incomplete GGUF tensor data: " + tensors_[i].name);
+        tensors_[i].file_offset = data_offset_ + offsets[i];
     }
     if (load_weights) {
         std::ifstream file(path_, std::ios::binary);
-        file.seekg(static_cast<std::streamoff>(data_offset_));
-        weights_.resize(in.size() - data_offset_);
+        file.seekg(static_cast<std::streamoff>(std::min(data_offset_, in.size())));
+        weights_.resize(data_offset_ < in.size() ? in.size() - data_offset_ : 0);
         if (!file.read(reinterpret_cast<char*>(weights_.data()), static_cast<std::streamsize>(weights_.size())))
             throw std::runtime_error("Failed to read GGUF data section");
     }

@@ -19,6 +19,8 @@ void check_status(int status, const char* what) {
     throw std::runtime_error(message);
 }
 
+void check_launch() { check_status(qk_check_launch(), "HIP kernel launch failed"); }
+
 int get_sm_count() {
     int count = 0;
     check_status(qk_device_info(nullptr, 0, &count, nullptr, 0), "HIP device query failed");
@@ -74,6 +76,25 @@ void matmul(const float* input, const Weight& weight, float* output, size_t rows
 
 void matmul(const float* input, const Weight& weight, float* output, size_t rows, const Stream& stream) {
     matmul(input, weight, output, rows, stream.get());
+}
+
+void rms_norm(const float* input, const Weight& scale, float* output, size_t rows, size_t width,
+              float epsilon) {
+    if (rows == 0) return;  // src/cuda/rms_norm.cu:31-34
+    if (width == 0 || !(epsilon > 0.0f) || scale.datatype != GGML_TYPE_F32 ||
+        scale.dimension.empty() || static_cast<size_t>(scale.dimension[0]) != width)
+        throw std::invalid_argument(
+            "RMSNorm requires an F32 scale matching the row width and positive epsilon");
+    check_status(qk_rms_norm(input, static_cast<const float*>(scale.device_buffer.data), output,
+                             static_cast<int64_t>(rows), static_cast<int64_t>(width), epsilon,
+                             nullptr),
+                 "HIP kernel launch failed");
+}
+
+void residual_add(float* state, const float* branch, size_t count) {
+    if (count == 0) return;  // src/cuda/residual_add.cu:16
+    check_status(qk_residual_add(state, branch, static_cast<int64_t>(count), nullptr),
+                 "HIP kernel launch failed");
 }
 
 void silu_multiply(const float* gate, const float* up, float* output, size_t count) {

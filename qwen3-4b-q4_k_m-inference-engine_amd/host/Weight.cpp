@@ -56,6 +56,10 @@ Weight::Weight(const GGUF& model, const std::string& tensor_name) : name(tensor_
     datatype = tensor->type;
     dimension.assign(tensor->dimensions.begin(), tensor->dimensions.end());
     const auto data = model.read_tensor_data(name);
+    // The kernels take the row count from dimension[1]: the bytes must hold
+    // exactly every row of every plane.
+    if (data.size() != gguf_tensor_bytes(datatype, tensor->dimensions))
+        throw std::runtime_error("GGUF tensor size does not match its dimensions: " + name);
     device_buffer = DeviceBuffer(data.data(), data.size());
 }
 

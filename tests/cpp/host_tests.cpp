@@ -154,4 +154,76 @@ TEST_CASE("GGUF reader parses metadata, tensor infos and data") {
     std::filesystem::remove(bad);
 }
 
+namespace {
+
+std::filesystem::path write_file(const char* name, const std::vector<unsigned char>& bytes) {
+    const auto path = std::filesystem::temp_directory_path() / name;
+    std::ofstream f(path, std::ios::binary);
+    f.write(reinterpret_cast<const char*>(bytes.data()), static_cast<std::streamsize>(bytes.size()));
+    return path;
+}
+
+GgufWriter header(uint64_t tensors) {
+    GgufWriter w;
+    w.out.insert(w.out.end(), {'G', 'G', 'U', 'F'});
+    w.pod<uint32_t>(3);
+    w.pod<uint64_t>(tensors);
+    w.pod<uint64_t>(0);  // no metadata: alignment 32
+    return w;
+}
+
+}  // namespace
+
+TEST_CASE("GGUF reader rejects a tensor whose byte size wraps") {
+    // ne = [256, 2^20, 2^22, 2^22]: 2^72 weights; 144 * 2^64 bytes wraps to 0 in 64 bits
+    GgufWriter w = header(1);
+    w.str("blk.0.wrapped.weight");
+    w.pod<uint32_t>(4);
+    for (int64_t ne : {int64_t{256}, int64_t{1} << 20, int64_t{1} << 22, int64_t{1} << 22}) w.pod<int64_t>(ne);
+    w.pod<uint32_t>(GGML_TYPE_Q4_K);
+    w.pod<uint64_t>(0);
+    while (w.out.size() % 32) w.out.push_back(0);
+    w.out.resize(w.out.size() + 144, 0);
+    const auto path = write_file("qk_host_test_wrap.gguf", w.out);
+    REQUIRE_THROWS_AS(GGUF{path}, std::runtime_error);
+    std::filesystem::remove(path);
+    std::array<int64_t, GGUF_MAX_DIMS> ne{256, int64_t{1} << 20, int64_t{1} << 22, int64_t{1} << 22};
+    REQUIRE_THROWS_AS(gguf_tensor_bytes(GGML_TYPE_Q4_K, ne), std::runtime_error);
+    ne = {2560, 9728, 1, 1};
+    REQUIRE(gguf_tensor_bytes(GGML_TYPE_Q4_K, ne) == std::size_t{9728} * 10 * 144);
+}
+
+TEST_CASE("GGUF reader takes a header-only file and rejects a misaligned tensor") {
+    // no tensors and no data padding: the data section is empty, not negative
+    GgufWriter w = header(0);
+    const auto path = write_file("qk_host_test_empty.gguf", w.out);
+    const GGUF model(path, true);
+    REQUIRE(model.get_tensors().empty());
+    REQUIRE(!model.has_weights());
+    std::filesystem::remove(path);
+
+    GgufWriter m = header(1);
+    m.str("blk.0.ffn_gate.weight");
+    m.pod<uint32_t>(2);
+    m.pod<int64_t>(256);
+    m.pod<int64_t>(1);
+    m.pod<uint32_t>(GGML_TYPE_Q4_K);
+    m.pod<uint64_t>(16);  // not a multiple of the 32-byte alignment
+    while (m.out.size() % 32) m.out.push_back(0);
+    m.out.resize(m.out.size() + 16 + 144, 0);
+    const auto bad = write_file("qk_host_test_misaligned.gguf", m.out);
+    REQUIRE_THROWS_AS(GGUF{bad}, std::runtime_error);
+    std::filesystem::remove(bad);
+
+    GgufWriter t = header(1);  // a tensor but the file ends inside the header padding
+    t.str("x");
+    t.pod<uint32_t>(1);
+    t.pod<int64_t>(256);
+    t.pod<uint32_t>(GGML_TYPE_Q4_K);
+    t.pod<uint64_t>(0);
+    const auto cut = write_file("qk_host_test_cut.gguf", t.out);
+    REQUIRE_THROWS_AS(GGUF{cut}, std::runtime_error);
+    std::filesystem::remove(cut);
+}
+
 int main() { return mini::run_all(); }

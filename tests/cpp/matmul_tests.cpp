@@ -13,6 +13,7 @@
 #include <limits>
 #include <vector>
 
+#include "EmbedLookup.hpp"
 #include "GGUF.hpp"
 #include "Kernels.hpp"
 #include "Weight.hpp"
@@ -215,6 +216,105 @@ TEST_CASE("Weights load from a GGUF file and dequantize bit-exactly") {
     copy_to_host(out, actual);
     REQUIRE(std::memcmp(actual.data(), expected.data(), actual.size() * sizeof(float)) == 0);
     std::filesystem::remove(path);
+}
+
+namespace {
+
+// A GGUF v3 file with one 2-D tensor (default alignment 32).
+std::filesystem::path write_gguf(const char* file_name, const std::string& tensor, ggml_type type,
+                                 int64_t width, int64_t rows, const std::vector<unsigned char>& bytes) {
+    std::vector<unsigned char> file;
+    auto pod = [&](auto v) {
+        const auto* p = reinterpret_cast<const unsigned char*>(&v);
+        file.insert(file.end(), p, p + sizeof(v));
+    };
+    auto str = [&](const std::string& s) {
+        pod(uint64_t(s.size()));
+        file.insert(file.end(), s.begin(), s.end());
+    };
+    file.insert(file.end(), {'G', 'G', 'U', 'F'});
+    pod(uint32_t(3)); pod(uint64_t(1)); pod(uint64_t(0));
+    str(tensor); pod(uint32_t(2)); pod(int64_t(width)); pod(int64_t(rows));
+    pod(uint32_t(type)); pod(uint64_t(0));
+    while (file.size() % 32) file.push_back(0);
+    file.insert(file.end(), bytes.begin(), bytes.end());
+    const auto path = std::filesystem::temp_directory_path() / file_name;
+    std::ofstream f(path, std::ios::binary);
+    f.write(reinterpret_cast<const char*>(file.data()), static_cast<std::streamsize>(file.size()));
+    return path;
+}
+
+}  // namespace
+
+TEST_CASE("EmbedLookup gathers rows in input order and dequantizes them bit-exactly") {
+    // src/tests/EmbedLookupTests.cpp:10-52 on a synthetic token_embd of each storage type
+    for (const ggml_type type : {GGML_TYPE_Q6_K, GGML_TYPE_Q4_K, GGML_TYPE_F32}) {
+        const int64_t width = 2560, vocabulary = 64;
+        const int64_t row_bytes = ggml_row_bytes(type, width);
+        std::vector<unsigned char> table(static_cast<size_t>(row_bytes * vocabulary));
+        if (type == GGML_TYPE_F32) {
+            for (size_t i = 0; i < table.size() / 4; ++i) {
+                const float v = std::sin(float(i) * 0.37f);
+                std::memcpy(table.data() + 4 * i, &v, 4);
+            }
+        } else {
+            qko_synth_superblocks(table.data(), type, vocabulary, width, 4242 + type,
+                                  type == GGML_TYPE_Q4_K ? 0.01f : 0.005f, 0.01f);
+        }
+        const auto path = write_gguf("qk_embed_test.gguf", "token_embd.weight", type, width, vocabulary, table);
+        const GGUF model(path);
+        const EmbedLookup lookup(model);
+        REQUIRE(lookup.get_embedding_size() == size_t(width));
+        REQUIRE(lookup.get_vocabulary_size() == size_t(vocabulary));
+        REQUIRE(lookup.get_row_bytes() == size_t(row_bytes));
+        const auto empty = lookup.lookup({});
+        REQUIRE(empty.bytes == 0 && empty.data == nullptr);
+        REQUIRE_THROWS_AS(lookup.lookup({std::numeric_limits<uint32_t>::max()}), std::out_of_range);
+        REQUIRE_THROWS_AS(lookup.lookup({3, 64}), std::out_of_range);
+        std::vector<uint32_t> ids;  // repeated ids, out of order
+        for (uint32_t i = 0; i < 32; ++i) ids.push_back(i % 3 == 0 ? 42 : i % 3 == 1 ? 7 : 63 - i);
+        const auto device = lookup.lookup(ids);
+        REQUIRE(device.bytes == ids.size() * width * sizeof(float));
+        std::vector<float> actual(ids.size() * width), expected(width);
+        REQUIRE(qk_memcpy_d2h(actual.data(), device.data, device.bytes, nullptr) == QK_OK);
+        for (size_t r = 0; r < ids.size(); ++r) {
+            const unsigned char* row = table.data() + ids[r] * row_bytes;
+            if (type == GGML_TYPE_F32) std::memcpy(expected.data(), row, width * 4);
+            else REQUIRE(qko_dequantize_rows(row, expected.data(), 1, width, row_bytes, type) == 0);
+            REQUIRE(std::memcmp(actual.data() + r * width, expected.data(), width * sizeof(float)) == 0);
+        }
+        std::filesystem::remove(path);
+    }
+}
+
+TEST_CASE("rms_norm and residual_add match the CPU oracle") {
+    // src/cuda/rms_norm.cu:6-36 and src/cuda/residual_add.cu:6-20
+    const size_t rows = 5, width = 2560;
+    const float eps = 1e-6f;
+    std::vector<float> x(rows * width), scale(width), branch(rows * width);
+    for (size_t i = 0; i < x.size(); ++i) {
+        x[i] = std::sin(float(i) * 0.031f) * (1.0f + float(i % 7));
+        branch[i] = std::cos(float(i) * 0.017f);
+    }
+    for (size_t i = 0; i < width; ++i) scale[i] = 1.0f + 0.5f * std::sin(float(i));
+    const Weight norm("blk.0.ffn_norm.weight", GGML_TYPE_F32, {int64_t(width)}, scale.data(), width * 4);
+    DeviceBuffer xd(x.data(), x.size() * 4), out(x.size() * 4), bd(branch.data(), branch.size() * 4);
+    kernels::rms_norm(static_cast<float*>(xd.data), norm, static_cast<float*>(out.data), rows, width, eps);
+    std::vector<float> got(x.size()), expected(x.size());
+    copy_to_host(out, got);
+    qko_rms_norm(x.data(), scale.data(), expected.data(), rows, width, eps);
+    for (size_t i = 0; i < got.size(); ++i)
+        REQUIRE(std::fabs(got[i] - expected[i]) <= 2e-6f * std::fabs(expected[i]) + 1e-30f);
+    REQUIRE_THROWS_AS(kernels::rms_norm(static_cast<float*>(xd.data), norm, static_cast<float*>(out.data),
+                                        rows, width + 256, eps),
+                      std::invalid_argument);  // scale width mismatch
+    REQUIRE_THROWS_AS(kernels::rms_norm(static_cast<float*>(xd.data), norm, static_cast<float*>(out.data),
+                                        rows, width, 0.0f),
+                      std::invalid_argument);
+    kernels::residual_add(static_cast<float*>(xd.data), static_cast<float*>(bd.data), x.size());
+    copy_to_host(xd, got);
+    for (size_t i = 0; i < got.size(); ++i) REQUIRE(got[i] == x[i] + branch[i]);
+    kernels::detail::check_launch();
 }
 
 int main() { return mini::run_all(); }

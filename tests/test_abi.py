@@ -55,6 +55,7 @@ def test_version_and_last_error_start_clean(qk):
     (12, 2560, 0, 1, 1),        # N = 0
     (14, 2560, -3, 1, 1),       # N < 0
     (12, 2560, 8, -1, 1),       # negative rows
+    (12, (1 << 30) + 256, 8, 1, 1),  # K beyond the kernels' 32-bit indexing
 ])
 def test_matmul_validation_matches_reference(qk, qtype, K, N, M, code):
     lib = qk.load()
@@ -142,3 +143,33 @@ def test_cpp_host_layer_validation():
     res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     print(res.stdout[-2000:], res.stderr[-2000:])
     assert res.returncode == 0
+
+
+def test_engine_call_sequence_builds_against_the_headers(tmp_path):
+    """tests/cpp/engine_calls.cpp: the reference engine's call sequence
+    (src/Engine.cpp:55-111) compiles against include/ and links against
+    libqk_engine.so with only rope and attention left to the engine."""
+    build = ROOT / "qwen3-4b-q4_k_m-inference-engine_amd" / "_build"
+    assert (build / "libqk_engine.so").exists(), "build the package first"
+    exe = tmp_path / "engine_calls"
+    cmd = ["g++", "-std=c++20", "-O0", "-Wall", "-Wextra", "-Werror", "-I", str(ROOT / "include"),
+           str(ROOT / "tests" / "cpp" / "engine_calls.cpp"), "-o", str(exe), "-L", str(build),
+           "-lqk_engine", "-lqk_hip", f"-Wl,-rpath,{build}"]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    print(res.stdout[-4000:], res.stderr[-4000:])
+    assert res.returncode == 0
+    assert exe.exists()
+
+
+def test_rms_norm_and_residual_add_validation(qk):
+    """src/cuda/rms_norm.cu:31-34 and src/cuda/residual_add.cu:16: zero rows or
+    count return at once; a zero width or non-positive epsilon is rejected."""
+    lib = qk.load()
+    assert lib.qk_rms_norm(None, None, None, 0, 2560, 1e-6, None) == 0
+    assert lib.qk_rms_norm(8, 8, 8, 1, 0, 1e-6, None) == 1
+    assert lib.qk_rms_norm(8, 8, 8, 1, 2560, 0.0, None) == 1
+    assert lib.qk_rms_norm(8, 8, 8, 1, 2560, float("nan"), None) == 1
+    assert lib.qk_rms_norm(None, 8, 8, 1, 2560, 1e-6, None) == 1
+    assert lib.qk_residual_add(None, None, 0, None) == 0
+    assert lib.qk_residual_add(8, 8, -1, None) == 1
+    assert lib.qk_residual_add(None, 8, 5, None) == 1

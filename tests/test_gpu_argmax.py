@@ -70,8 +70,10 @@ def test_argmax_validation(gpu):
 
 @pytest.mark.parametrize("qtype,K,N", [(Q6, 2560, 151936), (Q4, 2560, 9728), (Q6, 9728, 2560), (Q4, 256, 77)])
 def test_matmul_argmax_matches_matmul_then_argmax(gpu, oracle, qtype, K, N):
-    """The fused launch gives the matmul's logits and their argmax; the index is
-    also the oracle product's argmax whenever the top two are clearly apart."""
+    """The fused launch gives the matmul's logits and their argmax; its logits
+    are within the bar of the oracle product, and its index is the oracle
+    product's argmax whenever the top two are clearly apart (the full lm_head
+    151936 x 2560 included)."""
     qk = gpu
     print(f"[case] type={qtype} K={K} N={N}", flush=True)
     w = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
@@ -85,17 +87,19 @@ def test_matmul_argmax_matches_matmul_then_argmax(gpu, oracle, qtype, K, N):
     qk.matmul_argmax(x, w, qtype, K, N, logits, res, ws, n)
     qk.matmul_argmax(x, w, qtype, K, N, None, res2, ws, n)  # logits not written
     qk.synchronize()
+    print(f"[case] launch {qk.last_launch()}", flush=True)
     got = logits.download(np.float32)
     mm = ref_logits.download(np.float32)
     assert oracle.row_norm_error(got.reshape(1, N), mm.reshape(1, N).astype(np.float64)) <= 1e-6
     idx = int(res.download(np.uint32)[0])
     assert idx == oracle.argmax(got)
     assert int(res2.download(np.uint32)[0]) == idx
-    if N * qk.row_bytes(qtype, K) <= 64 << 20:
-        ref = oracle.reference_product(x.download(np.float32), w.download(np.uint8), qtype, K, N)[0]
-        top = np.sort(ref)[-2:]
-        if top[1] - top[0] > 1e-4 * abs(top[1]):
-            assert idx == int(np.argmax(ref))
+    ref = oracle.reference_product(x.download(np.float32), w.download(np.uint8), qtype, K, N)[0]
+    assert oracle.row_norm_error(got.reshape(1, N), ref.reshape(1, N)) <= 1e-5
+    top = np.sort(ref)[-2:]
+    print(f"[case] oracle top two {top[1]:.6g} {top[0]:.6g}, fused index {idx}, oracle {int(np.argmax(ref))}")
+    assert top[1] - top[0] > 1e-4 * abs(top[1])  # these seeds keep the top two 3-15% apart
+    assert idx == int(np.argmax(ref))
 
 
 def test_matmul_argmax_tie_goes_to_the_lower_row(gpu, oracle):

@@ -190,10 +190,40 @@ def test_matmul_m1_qwen3_shapes(gpu, oracle, name):
     assert_parity(oracle, got, ref)
 
 
+_BATCH_WEIGHTS: dict = {}
+
+
+def batch_weight(qk, oracle, name):
+    """One weight per Qwen3 shape for the batched cases (device buffer and host bytes)."""
+    if name not in _BATCH_WEIGHTS:
+        qtype, K, N = SHAPES[name]
+        w = make_weight(qk, oracle, qtype, N, K, SEED + 900 + list(SHAPES).index(name))
+        _BATCH_WEIGHTS[name] = (w, w.download(np.uint8))
+    return _BATCH_WEIGHTS[name]
+
+
+@pytest.mark.parametrize("name", ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate",
+                                  "ffn_down", "lm_head"])
+@pytest.mark.parametrize("M", [2, 4, 8])
+def test_matmul_batched_qwen3_shapes(gpu, oracle, name, M):
+    """Batched decode (M = 2..8, the rows src/Engine.cpp:83-109 pass per step
+    when several sequences decode together) at every full Qwen3 shape. The
+    launcher picks the kernel, its lanes per row and depth from the shape, so
+    these are the instantiations the M = 8 decode sweep runs; the launch is
+    printed for the record."""
+    qtype, K, N = SHAPES[name]
+    w, w_host = batch_weight(gpu, oracle, name)
+    x = oracle.synth_normal(M * K, SEED + 40 + M)
+    got = run_matmul(gpu, w, qtype, K, N, x, M)
+    print(f"[case] {name} type={qtype} K={K} N={N} M={M} launch {gpu.last_launch()}", flush=True)
+    ref = oracle.reference_product(x, w_host, qtype, K, N)
+    assert_parity(oracle, got, ref)
+
+
 @pytest.mark.parametrize("qtype,K", [(Q4, 2560), (Q6, 2560), (Q4, 4096), (Q6, 9728)])
 @pytest.mark.parametrize("rows", [1, 4, 5, 101])
 def test_matmul_rows_truncated_columns(gpu, oracle, qtype, K, rows):
-    """src/tests/MatmulTests.cpp:165-213: N = 19 of a larger tensor, sentinels."""
+    """src/tests/MatmulTests.cpp:84-132: N = 19 of a larger tensor, sentinels."""
     print(f"[case] type={qtype} K={K} rows={rows}", flush=True)
     N_full, N = 64, 19
     w = make_weight(gpu, oracle, qtype, N_full, K, SEED + 3)
@@ -220,7 +250,7 @@ def test_matmul_rows_truncated_columns(gpu, oracle, qtype, K, rows):
 
 @pytest.mark.parametrize("qtype", [Q4, Q6])
 def test_matmul_overwrite_and_concurrent_streams(gpu, oracle, qtype):
-    """src/tests/MatmulTests.cpp:93-163 on synthetic weights (K full width, N = 5, M = 3)."""
+    """src/tests/MatmulTests.cpp:12-82 on synthetic weights (K full width, N = 5, M = 3)."""
     K, N, M = (2560, 5, 3)
     w = make_weight(gpu, oracle, qtype, 16, K, SEED + 4)
     x = np.sin(np.arange(M * K, dtype=np.float32) * np.float32(0.031)).astype(np.float32) * np.float32(0.1)
@@ -296,6 +326,7 @@ def test_matmul_segments_qkv(gpu, oracle, M):
     ys = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes]
     gpu.matmul_segments(xd, M, K, [(w, q, N, y) for w, (q, N), y in zip(ws, shapes, ys)])
     gpu.synchronize()
+    print(f"[case] qkv M={M} launch {gpu.last_launch()}", flush=True)
     for w, (q, N), y in zip(ws, shapes, ys):
         got = y.download(np.float32).reshape(M, N)
         ref = oracle.reference_product(x, w.download(np.uint8), q, K, N)
@@ -305,7 +336,8 @@ def test_matmul_segments_qkv(gpu, oracle, M):
         assert oracle.row_norm_error(single, got.astype(np.float64)) <= 1e-6
 
 
-@pytest.mark.parametrize("qtype,M", [(Q4, 1), (Q4, 5), (Q6, 2), (Q4, 64), (Q6, 17)])
+@pytest.mark.parametrize("qtype,M", [(Q4, 1), (Q4, 2), (Q4, 4), (Q4, 5), (Q4, 8), (Q6, 2), (Q6, 8),
+                                     (Q4, 64), (Q6, 17)])
 def test_ffn_gate_up_silu(gpu, oracle, qtype, M):
     """SiLU(gate) * up of src/Engine.cpp:98-100 in one launch (M > 8: gate and up
     through one GEMM launch, then the SiLU kernel)."""
@@ -317,6 +349,7 @@ def test_ffn_gate_up_silu(gpu, oracle, qtype, M):
     h = gpu.DeviceBuffer(4 * M * N)
     gpu.ffn_gate_up(xd, gate, up, qtype, K, N, h, M)
     gpu.synchronize()
+    print(f"[case] ffn type={qtype} M={M} launch {gpu.last_launch()}", flush=True)
     got = h.download(np.float32).reshape(M, N)
     g = oracle.reference_product(x, gate.download(np.uint8), qtype, K, N)
     u = oracle.reference_product(x, up.download(np.uint8), qtype, K, N)

@@ -140,7 +140,7 @@ def test_prefill_ragged_against_oracle(gpu, oracle, qtype, M, N, K):
 
 @pytest.mark.parametrize("qtype", [Q4, Q6])
 def test_prefill_zero_input_and_reuse(gpu, oracle, qtype):
-    """src/tests/MatmulTests.cpp:93-163 at M > 8: zero rows give exact zeros,
+    """src/tests/MatmulTests.cpp:12-82 and :84-132 at M > 8: zero rows give exact zeros,
     a reused output is overwritten, two streams give identical bits."""
     K, N, M = 2560, 200, 40
     w = make_weight(gpu, qtype, N, K, SEED + 30)
