@@ -107,6 +107,21 @@ size_t qk_matmul_workspace_size(int type, int64_t K, int64_t N, int64_t M);
 int qk_matmul_ws(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
                  int64_t M, void *workspace, size_t workspace_bytes, qk_stream_t stream);
 
+/* Bytes of the device scratch array behind qk_matmul_noalloc (48 MiB: the
+ * prefill workspace of every Qwen3-4B projection up to M = 512 fits). */
+#define QK_NOALLOC_SCRATCH_BYTES ((size_t)48 << 20)
+
+/* qk_matmul that allocates nothing, for callers that cannot call hipMalloc
+ * (code under graph capture, tight serving loops, harnesses that forbid
+ * allocation). No counterpart in the reference. Same validation and results
+ * as qk_matmul; at M > 8 the prefill workspace is a file-scope device array of
+ * QK_NOALLOC_SCRATCH_BYTES per device (held until the process ends), so shapes
+ * whose qk_matmul_workspace_size exceeds it return QK_ERR_INVALID_ARGUMENT.
+ * All calls on one device share that array: calls that overlap on one device
+ * (e.g. on two streams) race. */
+int qk_matmul_noalloc(const float *x, const void *w, int type, int64_t K, int64_t N, float *y,
+                      int64_t M, qk_stream_t stream);
+
 /* Step 1 of qk_matmul: x[M x K] -> M*K/32 qk_q8_block (K % 32 == 0).
  * Replaces the quantize kernel of src/cuda/matmul.cu:8-22 (+ the sums). */
 int qk_quantize_q8(const float *x, int64_t M, int64_t K, qk_q8_block *q8,

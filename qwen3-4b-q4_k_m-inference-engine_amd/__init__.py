@@ -59,6 +59,7 @@ _SIGNATURES = {
     "qk_version": [],
     "qk_matmul": [_c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _i64, _c_void_p],
     "qk_matmul_workspace_size": [_int, _i64, _i64, _i64],
+    "qk_matmul_noalloc": [_c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _i64, _c_void_p],
     "qk_matmul_ws": [_c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _i64, _c_void_p, _size,
                      _c_void_p],
     "qk_quantize_q8": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
@@ -334,6 +335,11 @@ def matmul(x, w, qtype: int, K: int, N: int, y, M: int, stream=None, y_offset: i
     """y[M x N] = Q8(x)[M x K] . W^T  (qk_matmul; kernels::matmul)."""
     check(load().qk_matmul(_ptr(x), _ptr(w), qtype, K, N, _ptr(y, y_offset), M,
                            _stream_ptr(stream)))
+
+
+def matmul_noalloc(x, w, qtype: int, K: int, N: int, y, M: int, stream=None) -> None:
+    """qk_matmul_noalloc: qk_matmul with its prefill workspace in the library's device scratch."""
+    check(load().qk_matmul_noalloc(_ptr(x), _ptr(w), qtype, K, N, _ptr(y), M, _stream_ptr(stream)))
 
 
 def matmul_segments(x, M: int, K: int, segments, stream=None) -> None:

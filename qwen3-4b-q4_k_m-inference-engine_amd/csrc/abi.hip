@@ -186,6 +186,10 @@ int run_gemm_single(const float* x, const void* w, int type, int64_t K, int64_t 
 
 namespace qk {
 
+int set_error(int code, const char* message, hipError_t error) {
+  return error == hipSuccess ? fail(code, message) : hip_fail(error, message);
+}
+
 void note_launch(const char* kernel, int nvalues, const int* values, int64_t grid) {
   g_launch.kernel = kernel;
   g_launch.nvalues = std::min(nvalues, 6);

@@ -23,6 +23,10 @@ inline void note(const char* kernel, int64_t grid, T... values) {
   note_launch(kernel, static_cast<int>(sizeof...(T)), v, grid);
 }
 
+// Sets this thread's qk_last_error() message (with the HIP error's text
+// unless it is hipSuccess) and returns `code`.
+int set_error(int code, const char* message, hipError_t error);
+
 // One weight matrix of a mat-vec launch (rows = N, y is [M x N]).
 struct MatvecSegment {
   const uint8_t* w;
