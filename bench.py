@@ -84,8 +84,10 @@ class Op:
 class DecodeSweep:
     """Weights, activations and the per-token launch sequence of the decode sweep."""
 
-    def __init__(self, qk, M: int = 1, weights_of: "DecodeSweep | None" = None):
+    def __init__(self, qk, M: int = 1, weights_of: "DecodeSweep | None" = None, fused_ffn: bool = True):
         self.qk, self.M = qk, M
+        # M = 1: the FFN block (gate, up, SiLU*up, down) in one launch (qk_ffn)
+        self.fused_ffn = fused_ffn and M == 1
         if weights_of is not None:  # same weights, other activation rows
             self.layers, self.lm_head = weights_of.layers, weights_of.lm_head
         else:
@@ -114,6 +116,10 @@ class DecodeSweep:
         self.argmax_ws = qk.DeviceBuffer(self.argmax_bytes)
         qk.check(qk.load().qk_memset_async(self.argmax_ws.ptr, 0, self.argmax_bytes, None))
         self.next_token = qk.DeviceBuffer(4)
+        self.y_ffn = buf(2560)
+        self.ffn_ws_bytes = qk.ffn_workspace_size()
+        self.ffn_ws = qk.DeviceBuffer(self.ffn_ws_bytes)
+        qk.check(qk.load().qk_memset_async(self.ffn_ws.ptr, 0, self.ffn_ws_bytes, None))
         qk.synchronize()
 
     def ops(self, stream):
@@ -130,10 +136,17 @@ class DecodeSweep:
             w_o = layer["attn_output"]
             out.append(Op("attn_output", gemv_bytes(Q4, 4096, 2560, M),
                           lambda w=w_o: qk.matmul(self.x_o, w, Q4, 4096, 2560, y["attn_output"], M, stream)))
-            g, u = layer["ffn_gate"], layer["ffn_up"]
+            g, u, w_d = layer["ffn_gate"], layer["ffn_up"], layer["ffn_down"]
+            if self.fused_ffn:
+                # weights + x in + h out + y out (h's read-back inside the launch is not counted)
+                out.append(Op("ffn_block", 2 * weight_bytes(Q4, 2560, 9728) + weight_bytes(Q6, 9728, 2560)
+                              + 4 * M * (2560 + 9728 + 2560),
+                              lambda g=g, u=u, d=w_d: qk.ffn(self.x_ffn, None, 0.0, g, u, Q4, d, Q6, 2560, 9728,
+                                                             self.h, self.y_ffn, M, self.ffn_ws,
+                                                             self.ffn_ws_bytes, stream)))
+                continue
             out.append(Op("ffn_gate_up", 2 * weight_bytes(Q4, 2560, 9728) + 4 * M * (2560 + 9728),
                           lambda g=g, u=u: qk.ffn_gate_up(self.x_ffn, g, u, Q4, 2560, 9728, self.h, M, stream)))
-            w_d = layer["ffn_down"]
             out.append(Op("ffn_down", gemv_bytes(Q6, 9728, 2560, M),
                           lambda w=w_d: qk.matmul(self.h, w, Q6, 9728, 2560, y["ffn_down"], M, stream)))
         name, qtype, K, N = LM_HEAD
@@ -300,12 +313,15 @@ def measure_configs(qk, sweep: DecodeSweep, stream):
     """The other BASELINE configurations, reported beside the headline sweep."""
     out = {"0_q4k_gemv": single_gemv(qk, stream, Q4, 2560, 9728, 0),
            "1_q6k_gemv": single_gemv(qk, stream, Q6, 9728, 2560, 1)}
-    ffn = [op for op in sweep.ops(stream) if op.family in ("ffn_gate_up", "ffn_down")]
-    us = time_launches(qk, stream, [op.call for op in ffn]) * len(ffn)
-    nbytes = sum(op.nbytes for op in ffn)
-    out["2_ffn_block_sweep"] = {"shape": "36 x (gate+up SiLU, down), M=1", "us_per_sweep": round(us, 1),
-                                "GB/s": round(nbytes / (us * 1e3), 1),
-                                "frac": round(nbytes / (us * 1e3) / PEAK_HBM_GBS, 4)}
+    separate = DecodeSweep(qk, M=1, weights_of=sweep, fused_ffn=False)
+    for key, src, fams in (("2_ffn_block_sweep", sweep, ("ffn_block",)),
+                           ("2_ffn_block_sweep_two_launches", separate, ("ffn_gate_up", "ffn_down"))):
+        ffn = [op for op in src.ops(stream) if op.family in fams]
+        us = time_launches(qk, stream, [op.call for op in ffn]) * len(ffn)
+        nbytes = sum(op.nbytes for op in ffn)
+        out[key] = {"shape": f"36 x (gate+up SiLU, down), M=1, {len(ffn) // 36} launch(es) per layer",
+                    "us_per_sweep": round(us, 1), "us_per_layer": round(us / 36, 2),
+                    "GB/s": round(nbytes / (us * 1e3), 1), "frac": round(nbytes / (us * 1e3) / PEAK_HBM_GBS, 4)}
     out["3_prefill_gemm"] = prefill_gemm(qk, stream)
     sweep8 = DecodeSweep(qk, M=8, weights_of=sweep)
     graph = qk.Graph.capture(stream, lambda: sweep8.record(stream))
@@ -427,7 +443,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "Qwen3-4B Q4_K_M decode projection sweep, M=1: 36 x (q,k,v,o,gate,up,down) "
                                "+ lm_head 151936x2560 Q6_K with next-token argmax, Q8 activations, "
-                               "4 launches/layer + 1, graph-replayed",
+                               "3 launches/layer (qkv, o, FFN block) + 1, graph-replayed",
                    "tokens_per_s": round(1e3 / ms, 2), "bytes_per_step": bytes_step,
                    "frac_of_peak_hbm": round(gbs / PEAK_HBM_GBS, 4), "eager_ms_per_step": round(eager_ms, 3),
                    "device": info["name"], "arch": info["arch"]},

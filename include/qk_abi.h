@@ -158,6 +158,36 @@ int qk_ffn_gate_up_norm(const float *x, const float *norm, float eps, const void
                         const void *up, int type, int64_t K, int64_t N, float *h, int64_t M,
                         qk_stream_t stream);
 
+/* Bytes of the workspace qk_ffn needs (its grid-barrier words). The caller
+ * zero-fills it once before its first use; every call leaves it ready for the
+ * next. Calls that may run concurrently need separate workspaces. */
+size_t qk_ffn_workspace_size(void);
+
+/* The FFN block: h[M x N] = SiLU(Q8(x') . gate^T) * (Q8(x') . up^T) and
+ * y[M x K] = Q8(h) . down^T, with x' = RMSNorm(x) (scale `norm`: K device
+ * floats, eps > 0) or x itself when norm is NULL. gate and up: N rows of K
+ * (gate_up_type), down: K rows of N (down_type). Replaces rms_norm(ffn_norm),
+ * matmul(gate), matmul(up), silu_multiply, matmul(down) (src/Engine.cpp:97-101).
+ * M = 1 with Q4_K gate/up (the Q4_K_M layout) and shapes that fit one
+ * workgroup per CU: ONE launch. Phase 1 is the gate/up product (the norm
+ * folded in), each workgroup storing its range of h; a grid barrier; phase 2
+ * reads h back, quantises it and runs the down rows, whose weights were
+ * loaded during phase 1. That launch needs every workgroup resident at once:
+ * do not overlap it with other kernels on the device. Its barrier wait is
+ * bounded: if it ever times out, the outputs of that call are invalid and
+ * qk_ffn_workspace_check reports it. Other M or shapes: qk_ffn_gate_up(_norm)
+ * then qk_matmul on the stream (allocating at M > 8 as they do). Validation
+ * as qk_matmul for both weights, plus the workspace (256-byte aligned, at
+ * least qk_ffn_workspace_size bytes) and eps when norm is given. */
+int qk_ffn(const float *x, const float *norm, float eps, const void *gate, const void *up,
+           int gate_up_type, const void *down, int down_type, int64_t K, int64_t N, float *h,
+           float *y, int64_t M, void *workspace, size_t workspace_bytes, qk_stream_t stream);
+
+/* Synchronises `stream`, then returns QK_ERR_RUNTIME (and clears the flag) if
+ * a qk_ffn call on this workspace timed out in its grid barrier since the
+ * last check, else QK_OK. */
+int qk_ffn_workspace_check(void *workspace, qk_stream_t stream);
+
 /* Bytes of the workspace qk_argmax / qk_matmul_argmax need. The caller
  * zero-fills it once before its first use (qk_memset_async or hipMemset);
  * every call leaves it ready for the next. Calls that may run concurrently

@@ -69,6 +69,10 @@ _SIGNATURES = {
                        _c_void_p],
     "qk_ffn_gate_up_norm": [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _int, _i64, _i64,
                             _c_void_p, _i64, _c_void_p],
+    "qk_ffn_workspace_size": [],
+    "qk_ffn": [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _int, _c_void_p, _int, _i64, _i64,
+               _c_void_p, _c_void_p, _i64, _c_void_p, _size, _c_void_p],
+    "qk_ffn_workspace_check": [_c_void_p, _c_void_p],
     "qk_argmax_workspace_size": [],
     "qk_argmax": [_c_void_p, _i64, _c_void_p, _c_void_p, _size, _c_void_p],
     "qk_matmul_argmax": [_c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
@@ -108,7 +112,7 @@ _SIGNATURES = {
 }
 _RESTYPES = {"qk_last_error": ctypes.c_char_p, "qk_last_launch": ctypes.c_char_p,
              "qk_matmul_workspace_size": _size,
-             "qk_argmax_workspace_size": _size}
+             "qk_argmax_workspace_size": _size, "qk_ffn_workspace_size": _size}
 
 _LIB = None
 _SHUTTING_DOWN = False
@@ -335,6 +339,22 @@ def matmul(x, w, qtype: int, K: int, N: int, y, M: int, stream=None, y_offset: i
     """y[M x N] = Q8(x)[M x K] . W^T  (qk_matmul; kernels::matmul)."""
     check(load().qk_matmul(_ptr(x), _ptr(w), qtype, K, N, _ptr(y, y_offset), M,
                            _stream_ptr(stream)))
+
+
+def ffn_workspace_size() -> int:
+    return load().qk_ffn_workspace_size()
+
+
+def ffn(x, norm, eps: float, gate, up, gu_type: int, down, down_type: int, K: int, N: int, h, y,
+        M: int, workspace, workspace_bytes: int, stream=None) -> None:
+    """qk_ffn: h = SiLU(gate . x') * (up . x'), y = down . h (x' = RMSNorm(x) if norm)."""
+    check(load().qk_ffn(_ptr(x), _ptr(norm) if norm is not None else None, eps, _ptr(gate), _ptr(up),
+                        gu_type, _ptr(down), down_type, K, N, _ptr(h), _ptr(y), M, _ptr(workspace),
+                        workspace_bytes, _stream_ptr(stream)))
+
+
+def ffn_workspace_check(workspace, stream=None) -> None:
+    check(load().qk_ffn_workspace_check(_ptr(workspace), _stream_ptr(stream)))
 
 
 def matmul_noalloc(x, w, qtype: int, K: int, N: int, y, M: int, stream=None) -> None:

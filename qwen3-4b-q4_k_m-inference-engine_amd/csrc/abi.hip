@@ -385,6 +385,63 @@ int qk_ffn_gate_up_norm(const float* x, const float* norm, float eps, const void
   return result;
 }
 
+size_t qk_ffn_workspace_size(void) { return qk::ffn_sync_bytes(); }
+
+int qk_ffn(const float* x, const float* norm, float eps, const void* gate, const void* up,
+           int gate_up_type, const void* down, int down_type, int64_t K, int64_t N, float* h, float* y,
+           int64_t M, void* workspace, size_t workspace_bytes, qk_stream_t stream) {
+  int status = validate_matmul(gate_up_type, K, N, M);  // gate/up: N rows of width K
+  if (status != QK_OK) return status;
+  status = validate_matmul(down_type, N, K, M);  // down: K rows of width N
+  if (status != QK_OK) return status;
+  if (M == 0) return QK_OK;
+  if (norm && !(eps > 0.0f))  // src/cuda/rms_norm.cu:32
+    return fail(QK_ERR_INVALID_ARGUMENT, "RMSNorm requires a positive epsilon");
+  if (!x || !gate || !up || !down || !h || !y)
+    return fail(QK_ERR_INVALID_ARGUMENT, "ffn pointers must be non-null");
+  if (!workspace || workspace_bytes < qk::ffn_sync_bytes() ||
+      reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return fail(QK_ERR_INVALID_ARGUMENT,
+                "ffn workspace must be 256-byte aligned and hold qk_ffn_workspace_size() bytes");
+  for (const void* w : {gate, up}) {
+    status = validate_weight_pointer(w, gate_up_type);
+    if (status != QK_OK) return status;
+  }
+  status = validate_weight_pointer(down, down_type);
+  if (status != QK_OK) return status;
+  const hipStream_t s = as_stream(stream);
+  if (M == 1) {
+    const qk::FfnArgs a{x, norm, eps, gate, up, gate_up_type, down, down_type, K, N, h, y, workspace};
+    bool launched = false;
+    const hipError_t error = qk::launch_ffn_fused(a, s, launched);
+    if (error != hipSuccess) return hip_fail(error, "ffn launch failed");
+    if (launched) return QK_OK;
+  }
+  // Otherwise: the fused gate/up (with the norm when given), then down.
+  status = norm ? qk_ffn_gate_up_norm(x, norm, eps, gate, up, gate_up_type, K, N, h, M, stream)
+                : qk_ffn_gate_up(x, gate, up, gate_up_type, K, N, h, M, stream);
+  if (status != QK_OK) return status;
+  return qk_matmul(h, down, down_type, N, K, y, M, stream);
+}
+
+int qk_ffn_workspace_check(void* workspace, qk_stream_t stream) {
+  if (!workspace) return fail(QK_ERR_INVALID_ARGUMENT, "ffn workspace must be non-null");
+  uint32_t flag = 0;
+  const size_t at = 256;  // the timeout word's line
+  hipError_t error = hipMemcpyAsync(&flag, static_cast<char*>(workspace) + at, sizeof(flag),
+                                    hipMemcpyDeviceToHost, as_stream(stream));
+  if (error == hipSuccess) error = hipStreamSynchronize(as_stream(stream));
+  if (error != hipSuccess) return hip_fail(error, "ffn workspace read failed");
+  if (flag == 0) return QK_OK;
+  const uint32_t zero = 0;
+  error = hipMemcpyAsync(static_cast<char*>(workspace) + at, &zero, sizeof(zero), hipMemcpyHostToDevice,
+                         as_stream(stream));
+  if (error == hipSuccess) error = hipStreamSynchronize(as_stream(stream));
+  if (error != hipSuccess) return hip_fail(error, "ffn workspace reset failed");
+  return fail(QK_ERR_RUNTIME,
+              "ffn grid barrier timed out: not every workgroup was resident; outputs of that call are invalid");
+}
+
 size_t qk_argmax_workspace_size(void) { return qk::argmax_workspace_bytes(); }
 
 int qk_argmax(const float* logits, int64_t count, uint32_t* result, void* workspace,

@@ -52,6 +52,8 @@ std::mutex g_mutex;
 std::map<int, std::pair<int, int>> g_device;        // device -> (CUs, LDS bytes per workgroup)
 std::map<std::pair<const void*, int>, bool> g_lds;  // dynamic LDS limit set
 
+}  // namespace
+
 hipError_t device_limits(int& cus, int& max_lds) {
   int device = 0;
   hipError_t e = hipGetDevice(&device);
@@ -79,6 +81,8 @@ hipError_t allow_lds(const void* fn, int lds) {
   if (e == hipSuccess) g_lds.emplace(key, true);
   return e;
 }
+
+namespace {
 
 int type_bytes(int type) { return type == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes; }
 

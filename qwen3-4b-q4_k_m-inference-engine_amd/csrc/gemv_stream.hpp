@@ -100,14 +100,46 @@ __device__ __forceinline__ Q6KPiece lds_q6k_piece(const lds_u8* sb, uint32_t p) 
 
 // A wave's share: superblocks [sb_a, sb_b) of its part (MODE 1: waves 0-7
 // gate, 8-15 up) of the workgroup's rows, held as 16-byte chunks: lane l's
-// chunk j covers run bytes [off[j], off[j] + 16) from the dword boundary at or
+// chunk j covers run bytes [off(j), off(j) + 16) from the dword boundary at or
 // below the run start (o bytes before it; Q4_K runs are 16-byte aligned).
+// off(j) = 16 * min(l + 64 j, cmax), or lim for a chunk moved back to end at
+// the matrix's last dword boundary (recomputed where it is used rather than
+// held in J registers).
 template <int J>
 struct WaveShare {
   u32x4 chunk[J];
-  int off[J];
+  int cmax, lim;
   int sb_a, sb_b, o, part;
+  __device__ __forceinline__ int off(int j, int lane) const {
+    return min(16 * min(lane + 64 * j, cmax), lim);
+  }
 };
+
+// Issues the 16-byte loads of a wave's share: superblocks [sb_a, sb_b) of
+// rows [r0, ...) of a matrix of `rows` rows of S superblocks of B bytes at w
+// (dword-aligned). An empty share reads the run's first chunk. The matrix's
+// last chunk is moved back so it ends at the dword boundary at or above the
+// matrix end: no byte outside the matrix's dwords is read. (Addresses stay
+// pointer arithmetic on the kernel argument, so the compiler keeps them in
+// the global address space: global loads, whose waits count in order.)
+template <int J>
+__device__ __forceinline__ void issue_share(WaveShare<J>& ws, const uint8_t* w, int rows, int r0,
+                                            int S, int B, int lane) {
+  const int64_t row_bytes = static_cast<int64_t>(S) * B;
+  const uint8_t* run = w + r0 * row_bytes + static_cast<int64_t>(ws.sb_b > ws.sb_a ? ws.sb_a : 0) * B;
+  ws.o = static_cast<int>(reinterpret_cast<uintptr_t>(run) & 3u);  // 0 or 2 (Q6_K), 0 (Q4_K)
+  const uint8_t* run4 = run - ws.o;
+  ws.cmax = max((ws.o + (ws.sb_b - ws.sb_a) * B + 15) >> 4, 1) - 1;
+  // w is dword-aligned: the last dword boundary at or above the matrix end
+  const uint8_t* last = w + ((rows * row_bytes + 3) & ~int64_t{3}) - 16;
+  ws.lim = static_cast<int>(last - run4);
+#pragma unroll
+  for (int jj = 0; jj < J; ++jj) {
+    const uint8_t* a = run4 + 16 * min(lane + 64 * jj, ws.cmax);
+    a = a < last ? a : last;
+    ws.chunk[jj] = stream_load16_a4(a);
+  }
+}
 
 // Consumes the share after the activation barrier: chunks into the wave's
 // LDS region as they arrive (the waits count the loads issued after each
@@ -117,11 +149,20 @@ struct WaveShare {
 // IL: each round right after the chunks it needs (measured faster for the
 // mixed-type q/k/v launch); otherwise every chunk first, then the rounds.
 // SCALED: row totals are multiplied by out_scale (the RMSNorm fold).
-template <int TYPE, int J, int MODE, bool IL, bool SCALED = false>
+// AGENT_H: h is stored with agent-scope coherent stores (read back by other
+// workgroups of the same launch, the fused FFN). ROW_WAVE0, ROW_WAVES: the
+// waves that form the row totals. HOOK_AT: when >= 0
+// (non-IL only), hook() runs right after chunk HOOK_AT is in LDS (the fused
+// FFN issues its next loads there, once part of this share has arrived).
+struct NoHook {
+  __device__ __forceinline__ void operator()() const {}
+};
+template <int TYPE, int J, int MODE, bool IL, bool SCALED = false, bool AGENT_H = false,
+          int ROW_WAVE0 = 0, int ROW_WAVES = kStreamWaves, int HOOK_AT = -1, typename Hook = NoHook>
 __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, int max_sb, int r0,
                                                int r1, global_f32* yout, global_f32* hout,
                                                const lds_q8_block* xq, lds_u8* wlds,
-                                               lds_f32* sums, float out_scale) {
+                                               lds_f32* sums, float out_scale, Hook hook = Hook{}) {
   constexpr int B = TYPE == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes;
   const int lane = static_cast<int>(threadIdx.x & 63u);
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -153,10 +194,11 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
     if (s >= S) s -= S;
   };
   auto write_chunk = [&](int j) {
-    if (TYPE == QK_TYPE_Q4_K || (ws.off[j] & 15) == 0) {
-      *reinterpret_cast<lds_u32x4*>(reg + ws.off[j]) = ws.chunk[j];
+    const int off = ws.off(j, lane);
+    if (TYPE == QK_TYPE_Q4_K || (off & 15) == 0) {
+      *reinterpret_cast<lds_u32x4*>(reg + off) = ws.chunk[j];
     } else {
-      lds_u32* d = reinterpret_cast<lds_u32*>(reg + ws.off[j]);
+      lds_u32* d = reinterpret_cast<lds_u32*>(reg + off);
       d[0] = ws.chunk[j].x;
       d[1] = ws.chunk[j].y;
       d[2] = ws.chunk[j].z;
@@ -173,7 +215,14 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < J; ++j) write_chunk(j);
+    for (int j = 0; j < J; ++j) {
+      write_chunk(j);
+      if (j == HOOK_AT) {
+        __builtin_amdgcn_sched_barrier(0);  // the hook's loads stay after this chunk's wait
+        hook();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     asm volatile("" ::: "memory");  // the wave's reads below follow its writes
     for (int r = 0; r < rounds; ++r) compute(r);
   }
@@ -183,7 +232,16 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
   // sums k, k+4, ... in order, then the quad's DPP sum.
   const int nrows = r1 - r0;
   const int k = lane & 3;
-  for (int i = static_cast<int>(threadIdx.x) >> 2; i < nrows; i += 16 * kStreamWaves) {
+  const int rt = static_cast<int>(threadIdx.x) - 64 * ROW_WAVE0;
+  const int first = rt >= 0 && rt < 64 * ROW_WAVES ? rt >> 2 : nrows;
+  // When only some waves form the totals (the fused FFN, whose other waves go
+  // on to VALU-heavy work on the same SIMDs), they run at raised priority:
+  // sharing the SIMD evenly made one wave's 38 totals take ~2.5 us.
+  constexpr bool kPrio = ROW_WAVES < kStreamWaves;
+  if constexpr (kPrio) {
+    if (first < nrows) __builtin_amdgcn_s_setprio(3);
+  }
+  for (int i = first; i < nrows; i += 16 * ROW_WAVES) {
     float g = 0.0f, u = 0.0f;
     for (int t = k; t < S; t += 4) {
       g += sums[i * S + t];
@@ -196,10 +254,18 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
       u *= out_scale;
     }
     if (k == 0) {
-      if constexpr (MODE == 0) yout[r0 + i] = g;
-      else hout[r0 + i] = (g / (1.0f + expf(-g))) * u;
+      if constexpr (MODE == 0) {
+        yout[r0 + i] = g;
+      } else {
+        const float hv = (g / (1.0f + expf(-g))) * u;
+        if constexpr (AGENT_H)
+          __hip_atomic_store(hout + r0 + i, hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          hout[r0 + i] = hv;
+      }
     }
   }
+  if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
 }
 
 // TYPE: the weight type of every segment, or 0 for segments of both types.
@@ -271,12 +337,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
     asm volatile("" : "+s"(eps));
   }
 
-  // The wave's run [sb_a, sb_b) as 16-byte chunks. An idle wave reads the
-  // workgroup's first chunk. The last chunk of the matrix is moved back so it
-  // ends at the dword boundary at or above the matrix end: no byte outside
-  // the matrix's dwords is read. (Addresses stay pointer arithmetic on the
-  // kernel argument, so the compiler keeps them in the global address space:
-  // global loads, whose waits count in order.)
+  // The wave's run [sb_a, sb_b) as 16-byte chunks (an idle wave reads the
+  // workgroup's first chunk).
   const int B = type == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes;
   WaveShare<J> ws;
   ws.part = wave / kWpp;
@@ -284,22 +346,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_matvec_kernel(const 
   const int nsb = (r1 - r0) * S;  // superblocks of the workgroup, per part
   ws.sb_a = nsb * wv / kWpp;
   ws.sb_b = nsb * (wv + 1) / kWpp;
-  const uint8_t* w = kFfn && ws.part ? p.seg[1].w : w0;
-  const int64_t row_bytes = static_cast<int64_t>(S) * B;
-  const uint8_t* run = w + r0 * row_bytes + static_cast<int64_t>(ws.sb_b > ws.sb_a ? ws.sb_a : 0) * B;
-  ws.o = static_cast<int>(reinterpret_cast<uintptr_t>(run) & 3u);  // 0 or 2 (Q6_K), 0 (Q4_K)
-  const uint8_t* run4 = run - ws.o;
-  const int L = max((ws.o + (ws.sb_b - ws.sb_a) * B + 15) >> 4, 1);
-  // w is dword-aligned: the last dword boundary at or above the matrix end
-  const uint8_t* last = w + ((rows * row_bytes + 3) & ~int64_t{3}) - 16;
-#pragma unroll
-  for (int jj = 0; jj < J; ++jj) {
-    const int c = min(lane + 64 * jj, L - 1);
-    const uint8_t* a = run4 + 16 * c;
-    a = a < last ? a : last;
-    ws.off[jj] = static_cast<int>(a - run4);
-    ws.chunk[jj] = stream_load16_a4(a);
-  }
+  issue_share<J>(ws, kFfn && ws.part ? p.seg[1].w : w0, rows, r0, S, B, lane);
   __builtin_amdgcn_sched_barrier(0);
 
   lds_q8_block* xq = (lds_q8_block*)(lds_raw);

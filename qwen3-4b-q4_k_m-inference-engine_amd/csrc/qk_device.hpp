@@ -232,15 +232,18 @@ __device__ __forceinline__ float dot_q4k_piece(const Q4KPiece& w, const XFrag& x
          (main_b * rb.x - (dmin * static_cast<float>(m_b)) * rb.y);
 }
 
-// Q6_K piece p against the Q8 blocks of group r (xa) and group r+2 (xb) of
-// its half (src/cuda/matmul.cu:61-84):
-//   q = ((ql >> 4*(g/2)) & 15) | ((qh >> 2g) & 3) << 4, weight = d*sc*(q-32).
-// The -32 offset enters through the Q8 blocks' neg32 sums as the dots' start.
-__device__ __forceinline__ float dot_q6k_piece(const Q6KPiece& w, const XFrag& xa,
-                                               const XFrag& xb, uint32_t p) {
+// A Q6_K piece unpacked: the 6-bit codes of group r (a) and group r+2 (b) of
+// its half as bytes (32 each), the four int8 sub-block scales and d. Unpacking
+// needs no activations, so a kernel can do it ahead of them.
+struct Q6KCodes {
+  uint32_t a[8], b[8];
+  uint32_t sc;  // bytes: scale of a's first 16, a's last 16, b's first 16, b's last 16
+  float d;
+};
+
+// q = ((ql >> 4*(g/2)) & 15) | ((qh >> 2g) & 3) << 4 (src/cuda/matmul.cu:71-79).
+__device__ __forceinline__ Q6KCodes unpack_q6k_piece(const Q6KPiece& w, uint32_t p) {
   const uint32_t r = p & 1u;
-  const i32x4 ra = __builtin_bit_cast(i32x4, xa.rec);
-  const i32x4 rb = __builtin_bit_cast(i32x4, xb.rec);
   const uint32_t sh = w.shift;
   auto realign = [sh](uint32_t hi, uint32_t lo) { return __builtin_amdgcn_alignbit(hi, lo, sh); };
   const uint32_t l[8] = {realign(w.l0.y, w.l0.x), realign(w.l0.z, w.l0.y), realign(w.l0.w, w.l0.z),
@@ -249,32 +252,53 @@ __device__ __forceinline__ float dot_q6k_piece(const Q6KPiece& w, const XFrag& x
   const uint32_t q[8] = {realign(w.h0.y, w.h0.x), realign(w.h0.z, w.h0.y), realign(w.h0.w, w.h0.z),
                          realign(w.h1.x, w.h0.w), realign(w.h1.y, w.h1.x), realign(w.h1.z, w.h1.y),
                          realign(w.h1.w, w.h1.z), realign(w.h2, w.h1.w)};
-  const uint32_t ca[8] = {xa.c0.x, xa.c0.y, xa.c0.z, xa.c0.w, xa.c1.x, xa.c1.y, xa.c1.z, xa.c1.w};
-  const uint32_t cb[8] = {xb.c0.x, xb.c0.y, xb.c0.z, xb.c0.w, xb.c1.x, xb.c1.y, xb.c1.z, xb.c1.w};
   // rotate so bits (2g, 2g+1) of every qh byte land on bits 4 and 5
   const uint32_t rot_a = (2u * r - 4u) & 31u;  // g = r
   const uint32_t rot_b = 2u * r;               // g = r + 2: (2(r+2) - 4)
   constexpr uint32_t kLo = 0x0F0F0F0Fu, kHi = 0x30303030u;
+  Q6KCodes c;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    c.a[i] = (l[i] & kLo) | (__builtin_amdgcn_alignbit(q[i], q[i], rot_a) & kHi);
+    c.b[i] = ((l[i] >> 4) & kLo) | (__builtin_amdgcn_alignbit(q[i], q[i], rot_b) & kHi);
+  }
+  c.sc = (w.sc_a & 0xFFFFu) | (w.sc_b << 16);
+  c.d = half_bits_to_float(w.d_bits);
+  return c;
+}
+
+// An unpacked Q6_K piece against the Q8 blocks of group r (xa) and group r+2
+// (xb) of its half: weight = d*sc*(q-32); the -32 offset enters through the
+// Q8 blocks' neg32 sums as the dots' start.
+__device__ __forceinline__ float dot_q6k_codes(const Q6KCodes& c, const XFrag& xa, const XFrag& xb) {
+  const i32x4 ra = __builtin_bit_cast(i32x4, xa.rec);
+  const i32x4 rb = __builtin_bit_cast(i32x4, xb.rec);
+  const uint32_t ca[8] = {xa.c0.x, xa.c0.y, xa.c0.z, xa.c0.w, xa.c1.x, xa.c1.y, xa.c1.z, xa.c1.w};
+  const uint32_t cb[8] = {xb.c0.x, xb.c0.y, xb.c0.z, xb.c0.w, xb.c1.x, xb.c1.y, xb.c1.z, xb.c1.w};
   int a_lo = ra.z, a_hi = ra.w, b_lo = rb.z, b_hi = rb.w;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const uint32_t code_a = (l[i] & kLo) | (__builtin_amdgcn_alignbit(q[i], q[i], rot_a) & kHi);
-    const uint32_t code_b = ((l[i] >> 4) & kLo) | (__builtin_amdgcn_alignbit(q[i], q[i], rot_b) & kHi);
     if (i < 4) {
-      a_lo = dot4(code_a, ca[i], a_lo);
-      b_lo = dot4(code_b, cb[i], b_lo);
+      a_lo = dot4(c.a[i], ca[i], a_lo);
+      b_lo = dot4(c.b[i], cb[i], b_lo);
     } else {
-      a_hi = dot4(code_a, ca[i], a_hi);
-      b_hi = dot4(code_b, cb[i], b_hi);
+      a_hi = dot4(c.a[i], ca[i], a_hi);
+      b_hi = dot4(c.b[i], cb[i], b_hi);
     }
   }
   auto s8 = [](uint32_t v, int byte) { return static_cast<int>(static_cast<int8_t>((v >> (8 * byte)) & 0xFFu)); };
   // |sc*dot| <= 64*16*32*127 per group, each sum < 2^24: exact in fp32.
-  const int isum_a = __mul24(s8(w.sc_a, 0), a_lo) + __mul24(s8(w.sc_a, 1), a_hi);
-  const int isum_b = __mul24(s8(w.sc_b, 0), b_lo) + __mul24(s8(w.sc_b, 1), b_hi);
-  const float d = half_bits_to_float(w.d_bits);
-  return d * (__builtin_bit_cast(float, ra.x) * static_cast<float>(isum_a) +
-              __builtin_bit_cast(float, rb.x) * static_cast<float>(isum_b));
+  const int isum_a = __mul24(s8(c.sc, 0), a_lo) + __mul24(s8(c.sc, 1), a_hi);
+  const int isum_b = __mul24(s8(c.sc, 2), b_lo) + __mul24(s8(c.sc, 3), b_hi);
+  return c.d * (__builtin_bit_cast(float, ra.x) * static_cast<float>(isum_a) +
+                __builtin_bit_cast(float, rb.x) * static_cast<float>(isum_b));
+}
+
+// Q6_K piece p against the Q8 blocks of group r (xa) and group r+2 (xb) of
+// its half (src/cuda/matmul.cu:61-84).
+__device__ __forceinline__ float dot_q6k_piece(const Q6KPiece& w, const XFrag& xa,
+                                               const XFrag& xb, uint32_t p) {
+  return dot_q6k_codes(unpack_q6k_piece(w, p), xa, xb);
 }
 
 }  // namespace qk

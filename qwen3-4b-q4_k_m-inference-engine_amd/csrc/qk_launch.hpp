@@ -65,6 +65,34 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream);
 // otherwise nothing is enqueued and launch_matvec uses the streaming kernel.
 hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
 
+// Compute units and LDS bytes per workgroup of the current device (cached).
+hipError_t device_limits(int& cus, int& max_lds);
+// Sets a kernel's dynamic LDS limit to `lds` bytes (once per kernel and size).
+hipError_t allow_lds(const void* fn, int lds);
+
+// The FFN block of one activation row in one launch (ffn_fused.hip): h =
+// SiLU(Q8(x') . gate^T) * (Q8(x') . up^T) with x' = x or RMSNorm(x) (norm
+// non-null), then y = Q8(h) . down^T; sync is the barrier workspace. Launched
+// (and `launched` set) when the shapes fit its one-workgroup-per-CU plan;
+// otherwise nothing is enqueued.
+struct FfnArgs {
+  const float* x;
+  const float* norm;
+  float eps;
+  const void* gate;
+  const void* up;
+  int gate_up_type;
+  const void* down;
+  int down_type;
+  int64_t K, N;
+  float* h;
+  float* y;
+  void* sync;
+};
+hipError_t launch_ffn_fused(const FfnArgs& a, hipStream_t stream, bool& launched);
+// Bytes of the barrier workspace of launch_ffn_fused.
+size_t ffn_sync_bytes();
+
 // Activation rows one launch_matvec can take for width K (its Q8 blocks live
 // in LDS): 8, 4, 2 or 1, or 0 when even one row does not fit.
 int matvec_rows_per_launch(int64_t K);

@@ -1,0 +1,195 @@
+"""GPU parity of qk_ffn, the FFN block of src/Engine.cpp:97-101 (rms_norm of
+ffn_norm, gate, up, silu_multiply, down), against the CPU oracle and against
+the same block run as separate launches.
+
+At M = 1 with Q4_K gate/up the block is one launch with a grid barrier
+between the gate/up phase and the down phase. Bars: h within 1e-5 of the
+oracle's double-accumulated SiLU(gate) * up (row-norm error), y within 1e-5 of
+the oracle's reference product of the GPU's own h (the down product proper),
+and y within the path's 1e-3 of the oracle chain (a last-bit difference in h
+can move one Q8 code of the round trip). Since the fused launch runs the same
+row partition and the same fixed-order sums as the separate launches, both
+outputs are also bit-identical to qk_ffn_gate_up(_norm) + qk_matmul.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+Q4, Q6 = 12, 14
+SEED = 20261240
+DMAX = {Q4: 0.01, Q6: 0.005}
+
+
+def _weight(qk, qtype, N, K, seed):
+    w = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
+    qk.synth_superblocks(w, qtype, N, K, seed, DMAX[qtype], 0.01)
+    return w
+
+
+def _workspace(qk):
+    n = qk.ffn_workspace_size()
+    ws = qk.DeviceBuffer(n)
+    qk.check(qk.load().qk_memset_async(ws.ptr, 0, n, None))
+    return ws, n
+
+
+class Block:
+    def __init__(self, qk, oracle, K, N, down_type, M, norm, seed):
+        self.qk, self.K, self.N, self.down_type, self.M = qk, K, N, down_type, M
+        self.gate = _weight(qk, Q4, N, K, seed)
+        self.up = _weight(qk, Q4, N, K, seed + 1)
+        self.down = _weight(qk, down_type, K, N, seed + 2)
+        x = oracle.synth_normal(M * K, seed + 3) * np.float32(3.0)
+        self.x = x.astype(np.float32)
+        self.scale = None
+        if norm:
+            self.scale = (np.float32(1.0) + np.float32(0.3) * oracle.synth_normal(K, seed + 4)).astype(np.float32)
+        self.xd = qk.DeviceBuffer.from_array(self.x)
+        self.sd = qk.DeviceBuffer.from_array(self.scale) if norm else None
+        self.eps = 1e-6
+
+    def run(self, ws, nbytes, stream=None):
+        qk = self.qk
+        h = qk.DeviceBuffer.from_array(np.full(self.M * self.N, np.nan, np.float32))
+        y = qk.DeviceBuffer.from_array(np.full(self.M * self.K, np.nan, np.float32))
+        qk.ffn(self.xd, self.sd, self.eps, self.gate, self.up, Q4, self.down, self.down_type, self.K,
+               self.N, h, y, self.M, ws, nbytes, stream)
+        launch = qk.last_launch()
+        qk.synchronize(stream)
+        return (h.download(np.float32).reshape(self.M, self.N), y.download(np.float32).reshape(self.M, self.K),
+                launch)
+
+    def separate(self):
+        """The same block as separate launches (qk_ffn_gate_up(_norm), qk_matmul)."""
+        qk = self.qk
+        h = qk.DeviceBuffer(4 * self.M * self.N)
+        y = qk.DeviceBuffer(4 * self.M * self.K)
+        if self.sd is not None:
+            qk.ffn_gate_up_norm(self.xd, self.sd, self.eps, self.gate, self.up, Q4, self.K, self.N, h, self.M)
+        else:
+            qk.ffn_gate_up(self.xd, self.gate, self.up, Q4, self.K, self.N, h, self.M)
+        qk.matmul(h, self.down, self.down_type, self.N, self.K, y, self.M)
+        qk.synchronize()
+        return h.download(np.float32).reshape(self.M, self.N), y.download(np.float32).reshape(self.M, self.K)
+
+    def oracle_h(self, oracle):
+        xn = oracle.rms_norm(self.x, self.scale, self.K, self.eps) if self.scale is not None else self.x
+        g = oracle.reference_product(xn, self.gate.download(np.uint8), Q4, self.K, self.N)
+        u = oracle.reference_product(xn, self.up.download(np.uint8), Q4, self.K, self.N)
+        with np.errstate(over="ignore"):  # exp(-g) overflows to inf for very negative g: SiLU -> -0
+            return (g / (1.0 + np.exp(-g))) * u
+
+    def check(self, oracle, h, y):
+        h_ref = self.oracle_h(oracle)
+        err_h = oracle.row_norm_error(h, h_ref)
+        down = self.down.download(np.uint8)
+        y_own = oracle.reference_product(h, down, self.down_type, self.N, self.K)
+        y_chain = oracle.reference_product(h_ref.astype(np.float32), down, self.down_type, self.N, self.K)
+        err_y, err_chain = oracle.row_norm_error(y, y_own), oracle.row_norm_error(y, y_chain)
+        rate = oracle.approx_pass_rate(y, y_own)
+        print(f"h error {err_h:.3e}; y error vs oracle(h) {err_y:.3e} (Approx {rate:.5f}), vs oracle chain "
+              f"{err_chain:.3e}", flush=True)
+        assert err_h <= 1e-5
+        assert err_y <= 1e-5 and rate >= 0.999
+        assert err_chain <= 1e-3
+
+
+@pytest.mark.parametrize("down_type,norm", [(Q6, False), (Q6, True), (Q4, False), (Q4, True)])
+def test_ffn_block_qwen3_shape_one_launch(gpu, oracle, down_type, norm):
+    """Qwen3-4B FFN at M = 1: gate/up Q4_K 9728 x 2560, down 2560 x 9728."""
+    K, N = 2560, 9728
+    blk = Block(gpu, oracle, K, N, down_type, 1, norm, SEED + 10 * down_type + norm)
+    ws, nbytes = _workspace(gpu)
+    h, y, launch = blk.run(ws, nbytes)
+    print(f"[case] ffn K={K} N={N} down={down_type} norm={norm} launch {launch}", flush=True)
+    assert launch.startswith("ffn_fused_kernel")
+    blk.check(oracle, h, y)
+    hs, ys = blk.separate()
+    assert np.array_equal(h, hs) and np.array_equal(y, ys)
+    for _ in range(3):  # the barrier workspace is re-armed by every call
+        h2, y2, _ = blk.run(ws, nbytes)
+        assert np.array_equal(h2, h) and np.array_equal(y2, y)
+    gpu.ffn_workspace_check(ws)
+
+
+@pytest.mark.parametrize("K,N,down_type", [(1024, 3072, Q6), (2048, 6144, Q4), (512, 1024, Q6)])
+def test_ffn_block_other_shapes_one_launch(gpu, oracle, K, N, down_type):
+    blk = Block(gpu, oracle, K, N, down_type, 1, True, SEED + K + N)
+    ws, nbytes = _workspace(gpu)
+    h, y, launch = blk.run(ws, nbytes)
+    print(f"[case] ffn K={K} N={N} down={down_type} launch {launch}", flush=True)
+    assert launch.startswith("ffn_fused_kernel")
+    blk.check(oracle, h, y)
+    hs, ys = blk.separate()
+    assert np.array_equal(h, hs) and np.array_equal(y, ys)
+    gpu.ffn_workspace_check(ws)
+
+
+@pytest.mark.parametrize("M,norm", [(2, True), (8, False), (12, True)])
+def test_ffn_block_batched_rows_take_separate_launches(gpu, oracle, M, norm):
+    K, N = 2560, 9728
+    blk = Block(gpu, oracle, K, N, Q6, M, norm, SEED + 100 + M)
+    ws, nbytes = _workspace(gpu)
+    h, y, launch = blk.run(ws, nbytes)
+    print(f"[case] ffn M={M} launch {launch}", flush=True)
+    assert not launch.startswith("ffn_fused_kernel")
+    if M <= 8:
+        blk.check(oracle, h, y)
+    else:  # the prefill GEMM's fp16 split products: within the path's bar
+        h_ref = blk.oracle_h(oracle)
+        assert oracle.row_norm_error(h, h_ref) <= 1e-5
+        y_own = oracle.reference_product(h, blk.down.download(np.uint8), Q6, N, K)
+        assert oracle.row_norm_error(y, y_own) <= 1e-5
+
+
+def test_ffn_block_graph_replays(gpu, oracle):
+    """The one-launch block captured in a graph, replayed with eager calls and
+    synchronisations in between: every replay equals the eager result."""
+    qk = gpu
+    K, N = 2560, 9728
+    blk = Block(qk, oracle, K, N, Q6, 1, True, SEED + 300)
+    ws, nbytes = _workspace(qk)
+    stream = qk.Stream()
+    h = qk.DeviceBuffer(4 * N)
+    y = qk.DeviceBuffer(4 * K)
+
+    def record():
+        qk.ffn(blk.xd, blk.sd, blk.eps, blk.gate, blk.up, Q4, blk.down, Q6, K, N, h, y, 1, ws, nbytes, stream)
+
+    record()
+    stream.synchronize()
+    eager = (h.download(np.float32), y.download(np.float32))
+    graph = qk.Graph.capture(stream, lambda: [record() for _ in range(3)])
+    for rep in range(4):
+        y.upload(np.full(K, np.nan, np.float32))
+        h.upload(np.full(N, np.nan, np.float32))
+        graph.launch(stream)
+        stream.synchronize()
+        assert np.array_equal(h.download(np.float32), eager[0]), f"replay {rep}"
+        assert np.array_equal(y.download(np.float32), eager[1]), f"replay {rep}"
+        record()
+        stream.synchronize()
+    graph.destroy()
+    qk.ffn_workspace_check(ws, stream)
+    stream.destroy()
+
+
+def test_ffn_block_validation(gpu):
+    lib = gpu.load()
+    ws, nbytes = _workspace(gpu)
+    d = gpu.DeviceBuffer(1 << 16)
+    args = [d.ptr, None, 0.0, d.ptr, d.ptr, Q4, d.ptr, Q6, 2560, 9728, d.ptr, d.ptr, 1]
+    assert lib.qk_ffn(*args, ws.ptr, nbytes - 256, None) == 1          # workspace too small
+    assert lib.qk_ffn(*args, ws.ptr + 16, nbytes, None) == 1           # misaligned workspace
+    bad = list(args)
+    bad[1], bad[2] = d.ptr, 0.0                                        # norm without a positive eps
+    assert lib.qk_ffn(*bad, ws.ptr, nbytes, None) == 1
+    bad = list(args)
+    bad[7] = 13                                                        # Q5_K down
+    assert lib.qk_ffn(*bad, ws.ptr, nbytes, None) == 2
+    bad = list(args)
+    bad[12] = 0                                                        # no rows: nothing to do
+    assert lib.qk_ffn(*bad, ws.ptr, nbytes, None) == 0

@@ -288,3 +288,152 @@ def test_batched_ffn_down_takes_the_streaming_kernel():
 
 def test_batched_q6k_gate_up_too_wide_takes_the_streaming_kernel():
     assert launcher_mt([9728, 9728], [14, 14], 2560, 1, 2) is None  # 5 rows of 2100 B per wave: J > 8
+
+
+# ---- the fused FFN block (ffn_fused.hip / ffn_fused.hpp), M = 1 ----
+
+H_WAVES = 1           # the last wave: it stores h, its down share is empty
+JG_CHOICES = (2, 4, 6, 7, 8)
+JD_CHOICES = (2, 4, 6, 8)      # 16-byte chunks per lane of the down share
+PD_CHOICES = (1, 2, 3)         # Q6_K down: pieces per lane unpacked ahead of h
+Q6_PAIRS = {(2, 1), (4, 1), (4, 2), (6, 2), (8, 2), (8, 3)}  # instantiated (JD, PD)
+SYNC_BYTES = 8192
+
+
+def _round_up(j, choices):
+    return next((c for c in choices if j <= c), 0)
+
+
+def _depth(sb, nbytes):
+    return -(-(-(-(2 + sb * nbytes) // 16)) // 64)
+
+
+def ffn_launcher(K, N, down_type, gate_up_type=12):
+    """(G, per, rem, dper, drem, max_sb, max_sbd, JG, JD, PD, lds) or None (two-launch path)."""
+    if gate_up_type != 12 or K > MAX_K or N > MAX_K or K % 256 or N % 256:
+        return None
+    G = CUS
+    if G > N or G > K:
+        return None
+    S, Sd = K // 256, N // 256
+    per, rem, dper, drem = N // G, N % G, K // G, K % G
+    max_sb, max_sbd = (per + (1 if rem else 0)) * S, (dper + (1 if drem else 0)) * Sd
+    wpp, dwaves = WAVES // 2, WAVES - H_WAVES
+    jg = _round_up(_depth(-(-max_sb // wpp), 144), JG_CHOICES)
+    down_sb = -(-max_sbd // dwaves)
+    jd = _round_up(_depth(down_sb, BYTES[down_type]), JD_CHOICES)
+    pd = _round_up(-(-4 * down_sb // 64), PD_CHOICES) if down_type == 14 else 0
+    if jg == 0 or jd == 0 or (down_type == 14 and (pd == 0 or (jd, pd) not in Q6_PAIRS)) or jg + jd > 14:
+        return None
+    lds_a = S * 8 * 48 + WAVES * jg * 1024 + 2 * max_sb * 4 + 4 * WAVES
+    lds_b = Sd * 8 * 48 + WAVES * jd * 1024 + max_sbd * 4
+    lds = max(lds_a, lds_b)
+    if lds > MAX_LDS:
+        return None
+    return G, per, rem, dper, drem, max_sb, max_sbd, jg, jd, pd, lds
+
+
+def _share_reads(base, rows, r0, S, B, sb_a, sb_b, J):
+    """Global addresses and LDS offsets of one wave's issue_share (per lane, per chunk)."""
+    rb = S * B
+    run = base + r0 * rb + (sb_a if sb_b > sb_a else 0) * B
+    o = run & 3
+    run4 = run - o
+    cmax = max((o + (sb_b - sb_a) * B + 15) >> 4, 1) - 1
+    last = base + ((rows * rb + 3) & ~3) - 16
+    lim = last - run4
+    c = np.minimum(np.arange(64)[:, None] + 64 * np.arange(J)[None, :], cmax)
+    a = np.minimum(run4 + 16 * c, last)
+    off = np.minimum(16 * c, lim)
+    assert np.array_equal(off, a - run4)  # the lazily recomputed offset is the load's
+    end = base + rows * rb
+    assert np.all(a >= base) and np.all(a + 16 <= ((end + 3) & ~3)) and np.all(a % 4 == 0)
+    assert np.all(off >= 0) and np.all(off + 16 <= J * 1024)
+    cov_end = max(16 * cmax, min(16 * cmax, lim) + 16)
+    assert cov_end >= o + (sb_b - sb_a) * B
+    return o
+
+
+def check_ffn(K, N, down_type, bases):
+    cfg = ffn_launcher(K, N, down_type)
+    if cfg is None:
+        return False
+    G, per, rem, dper, drem, max_sb, max_sbd, JG, JD, PD, lds = cfg
+    S, Sd = K // 256, N // 256
+    wpp, dwaves = WAVES // 2, WAVES - H_WAVES
+    seen = np.zeros((2, N * S), np.int64)
+    seen_d = np.zeros(K * Sd, np.int64)
+    for g in range(G):
+        r0 = g * per + min(g, rem)
+        r1 = r0 + per + (1 if g < rem else 0)
+        d0 = g * dper + min(g, drem)
+        d1 = d0 + dper + (1 if g < drem else 0)
+        assert 0 <= r0 < r1 <= N and 0 <= d0 < d1 <= K
+        nsb, nsbd = (r1 - r0) * S, (d1 - d0) * Sd
+        assert nsb <= max_sb and nsbd <= max_sbd
+        for w in range(WAVES):
+            part, wv = w // wpp, w % wpp
+            sb_a, sb_b = nsb * wv // wpp, nsb * (wv + 1) // wpp
+            _share_reads(bases[part], N, r0, S, 144, sb_a, sb_b, JG)
+            seen[part, r0 * S + sb_a: r0 * S + sb_b] += 1
+            da, db = (nsbd * w // dwaves, nsbd * (w + 1) // dwaves) if w < dwaves else (0, 0)
+            o = _share_reads(bases[2], K, d0, Sd, BYTES[down_type], da, db, JD)
+            if down_type == 14:
+                # pieces read back from the wave's LDS region: lane q = l + 64 i takes piece q % 4
+                # of superblock q // 4 of the run (lanes past the share redo its last piece; an
+                # empty share reads piece 0); each read spans [base of the dword, superblock end)
+                npc = 4 * (db - da)
+                assert npc <= 64 * PD, "every piece of the share has a lane"
+                q = np.arange(64)[:, None] + 64 * np.arange(PD)[None, :]
+                qc = np.minimum(q, npc - 1) if npc > 0 else np.zeros_like(q)
+                start = o + (qc >> 2) * 210
+                assert np.all((start & ~3) >= 0) and np.all(start + 210 <= JD * 1024)
+                stored = (q < npc) & ((q & 3) == 0)
+                assert np.all(da + (q[stored] >> 2) < max_sbd)
+            seen_d[d0 * Sd + da: d0 * Sd + db] += 1
+            # piece reads of Q8 blocks: gate/up over K (x), down over N (h)
+            for (a_, b_, SS) in ((sb_a, sb_b, S), (da, db, Sd)):
+                q = np.arange(4 * (b_ - a_))
+                s = (a_ + (q >> 2)) % SS
+                assert np.all(s * 8 + 7 < SS * 8)
+        # row totals of phase A by the first H_WAVES waves, a quad per row
+        assert (r1 - r0) <= 10_000
+    assert np.all(seen == 1) and np.all(seen_d == 1), "every superblock exactly once"
+    # h staging: every task of 8 values staged by nqh waves, 2 tasks per lane
+    nqh = min(WAVES, -(-(N // 8) // (64 * XSTAGED)))
+    assert 64 * nqh * XSTAGED >= N // 8
+    # LDS: phase A (Q8 of x, wave regions, both parts' sums, norm partials);
+    # phase B (Q8 of h, wave regions, sums) reuse the same bytes
+    assert S * 8 * 48 + WAVES * JG * 1024 + 2 * max_sb * 4 + 4 * WAVES <= lds <= MAX_LDS
+    assert Sd * 8 * 48 + WAVES * JD * 1024 + max_sbd * 4 <= lds
+    # barrier words: 3 + 2 x 8 lines of 256 bytes
+    assert (3 + 2 * 8) * 256 <= SYNC_BYTES
+    return True
+
+
+FFN_SHAPES = [
+    (2560, 9728, 14),   # Qwen3-4B: gate/up Q4_K, down Q6_K
+    (2560, 9728, 12),   # Q4_K down (layers of Q4_K_M files that keep it at 4 bits)
+    (2048, 6144, 14),   # Qwen3-1.7B
+    (1024, 3072, 14),   # Qwen3-0.6B
+    (4096, 4096, 12),
+    (2816, 2560, 14),   # ragged rows per workgroup
+]
+
+
+@pytest.mark.parametrize("K,N,down_type", FFN_SHAPES)
+def test_fused_ffn_indices_in_bounds(K, N, down_type):
+    bases = [1 << 24, 2 << 24, (3 << 24) + (4 if down_type == 14 else 0)]
+    assert check_ffn(K, N, down_type, bases)
+
+
+def test_fused_ffn_plan_for_qwen3_4b():
+    G, per, rem, dper, drem, max_sb, max_sbd, JG, JD, PD, lds = ffn_launcher(2560, 9728, 14)
+    assert (per, rem, dper, drem, JG, JD, PD) == (38, 0, 10, 0, 7, 6, 2)
+    assert lds > MAX_LDS // 2  # one workgroup per CU
+
+
+def test_fused_ffn_declines_shapes_that_do_not_fit():
+    assert ffn_launcher(4096, 12288, 14) is None   # gate/up share too deep (Qwen3-8B)
+    assert ffn_launcher(2560, 9728, 14, gate_up_type=14) is None
+    assert ffn_launcher(2560, 20480, 14) is None   # h wider than the quantiser staging
