@@ -139,6 +139,18 @@ int qk_matmul_q8(const qk_q8_block *q8, const void *w, int type, int64_t K, int6
 int qk_matmul_segments(const float *x, int64_t M, int64_t K, const qk_segment *segments,
                        int count, qk_stream_t stream);
 
+/* Workspace bytes qk_matmul_segments_ws needs (0 for M <= 8 and for arguments
+ * qk_matmul_segments rejects): the largest of the segments' GEMM workspaces
+ * (they run one after another on one activation prep). */
+size_t qk_matmul_segments_workspace_size(int64_t M, int64_t K, const qk_segment *segments,
+                                         int count);
+
+/* qk_matmul_segments with a caller-owned device workspace (16-byte aligned, at
+ * least qk_matmul_segments_workspace_size bytes; may be NULL for M <= 8):
+ * allocates nothing, so a prefill can be captured into a graph. */
+int qk_matmul_segments_ws(const float *x, int64_t M, int64_t K, const qk_segment *segments,
+                          int count, void *workspace, size_t workspace_bytes, qk_stream_t stream);
+
 /* h[M x N] = SiLU(Q8(x) . gate^T) * (Q8(x) . up^T), gate and up both `type`
  * with K columns and N rows: one launch for M <= 8; for M > 8 the prefill
  * GEMM (gate and up in one launch) into stream-ordered scratch, then the
@@ -146,6 +158,18 @@ int qk_matmul_segments(const float *x, int64_t M, int64_t K, const qk_segment *s
  * (src/Engine.cpp:98-100, src/cuda/silu_multiply.cu:6-12). */
 int qk_ffn_gate_up(const float *x, const void *gate, const void *up, int type, int64_t K,
                    int64_t N, float *h, int64_t M, qk_stream_t stream);
+
+/* Workspace bytes qk_ffn_gate_up_ws needs (0 for M <= 8 and for shapes
+ * qk_ffn_gate_up rejects): gate and up outputs (2*M*N*4, rounded up to 256)
+ * and the GEMM workspace. */
+size_t qk_ffn_gate_up_workspace_size(int type, int64_t K, int64_t N, int64_t M);
+
+/* qk_ffn_gate_up with a caller-owned device workspace (16-byte aligned, at
+ * least qk_ffn_gate_up_workspace_size bytes; may be NULL for M <= 8):
+ * allocates nothing. Same results as qk_ffn_gate_up. */
+int qk_ffn_gate_up_ws(const float *x, const void *gate, const void *up, int type, int64_t K,
+                      int64_t N, float *h, int64_t M, void *workspace, size_t workspace_bytes,
+                      qk_stream_t stream);
 
 /* qk_ffn_gate_up on RMSNorm(x): each row x_m is first replaced by
  * (x_m * rsqrt(mean(x_m^2) + eps)) * norm (norm: K device floats). Replaces
@@ -276,9 +300,10 @@ int qk_event_elapsed_ms(float *ms, qk_event_t start, qk_event_t end);
  * call (the reference lists CUDA Graphs as future work, README.md:42). No
  * compute entry point records a memset. At M <= 8 none allocates, except
  * qk_ffn_gate_up_norm outside its M = 1 fold; at M > 8 qk_matmul,
- * qk_matmul_segments, qk_ffn_gate_up and qk_ffn_gate_up_norm allocate their
- * scratch stream-ordered (captured as allocation nodes), while the _ws entry
- * points take a caller workspace and allocate nothing.
+ * qk_matmul_segments, qk_ffn_gate_up, qk_ffn_gate_up_norm and qk_ffn allocate
+ * their scratch stream-ordered (captured as allocation nodes), while the _ws
+ * entry points take a caller workspace and qk_matmul_noalloc uses the
+ * library's scratch array: those allocate nothing.
  * ------------------------------------------------------------------------- */
 int qk_stream_begin_capture(qk_stream_t stream);
 /* Ends the capture and instantiates it; *graph owns the executable graph. */

@@ -67,6 +67,12 @@ _SIGNATURES = {
     "qk_matmul_segments": [_c_void_p, _i64, _i64, ctypes.POINTER(Segment), _int, _c_void_p],
     "qk_ffn_gate_up": [_c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _i64,
                        _c_void_p],
+    "qk_ffn_gate_up_workspace_size": [_int, _i64, _i64, _i64],
+    "qk_ffn_gate_up_ws": [_c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _i64,
+                          _c_void_p, _size, _c_void_p],
+    "qk_matmul_segments_workspace_size": [_i64, _i64, ctypes.POINTER(Segment), _int],
+    "qk_matmul_segments_ws": [_c_void_p, _i64, _i64, ctypes.POINTER(Segment), _int, _c_void_p, _size,
+                              _c_void_p],
     "qk_ffn_gate_up_norm": [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _int, _i64, _i64,
                             _c_void_p, _i64, _c_void_p],
     "qk_ffn_workspace_size": [],
@@ -112,7 +118,8 @@ _SIGNATURES = {
 }
 _RESTYPES = {"qk_last_error": ctypes.c_char_p, "qk_last_launch": ctypes.c_char_p,
              "qk_matmul_workspace_size": _size,
-             "qk_argmax_workspace_size": _size, "qk_ffn_workspace_size": _size}
+             "qk_argmax_workspace_size": _size, "qk_ffn_workspace_size": _size,
+             "qk_ffn_gate_up_workspace_size": _size, "qk_matmul_segments_workspace_size": _size}
 
 _LIB = None
 _SHUTTING_DOWN = False
@@ -366,6 +373,31 @@ def matmul_segments(x, M: int, K: int, segments, stream=None) -> None:
     """segments: [(w, qtype, N, y), ...] (qk_matmul_segments; q/k/v in one launch)."""
     arr = (Segment * len(segments))(*[Segment(_ptr(w), qtype, N, _ptr(y)) for w, qtype, N, y in segments])
     check(load().qk_matmul_segments(_ptr(x), M, K, arr, len(segments), _stream_ptr(stream)))
+
+
+def _segments(segments):
+    return (Segment * len(segments))(*[Segment(_ptr(w), qtype, N, _ptr(y)) for w, qtype, N, y in segments])
+
+
+def matmul_segments_workspace_size(M: int, K: int, segments) -> int:
+    return load().qk_matmul_segments_workspace_size(M, K, _segments(segments), len(segments))
+
+
+def matmul_segments_ws(x, M: int, K: int, segments, workspace, workspace_bytes: int, stream=None) -> None:
+    """qk_matmul_segments_ws: qk_matmul_segments with a caller workspace."""
+    check(load().qk_matmul_segments_ws(_ptr(x), M, K, _segments(segments), len(segments), _ptr(workspace),
+                                       workspace_bytes, _stream_ptr(stream)))
+
+
+def ffn_gate_up_workspace_size(qtype: int, K: int, N: int, M: int) -> int:
+    return load().qk_ffn_gate_up_workspace_size(qtype, K, N, M)
+
+
+def ffn_gate_up_ws(x, gate, up, qtype: int, K: int, N: int, h, M: int, workspace, workspace_bytes: int,
+                   stream=None) -> None:
+    """qk_ffn_gate_up_ws: qk_ffn_gate_up with a caller workspace."""
+    check(load().qk_ffn_gate_up_ws(_ptr(x), _ptr(gate), _ptr(up), qtype, K, N, _ptr(h), M, _ptr(workspace),
+                                   workspace_bytes, _stream_ptr(stream)))
 
 
 def ffn_gate_up(x, gate, up, qtype: int, K: int, N: int, h, M: int, stream=None) -> None:

@@ -269,8 +269,72 @@ int qk_matmul_q8(const qk_q8_block* q8, const void* w, int type, int64_t K, int6
   return run_single(nullptr, q8, w, type, K, N, y, M, as_stream(stream));
 }
 
-int qk_matmul_segments(const float* x, int64_t M, int64_t K, const qk_segment* segments, int count,
-                       qk_stream_t stream) {
+namespace {
+
+// Prefill FFN (M > 8): gate and up through the GEMM (one launch for both
+// where no split K is needed) into scratch, then SiLU(gate) * up into h. The
+// scratch (gate and up outputs, then the GEMM workspace) is the caller's
+// workspace when given, else allocated stream-ordered for the call.
+size_t ffn_gemm_bytes(int type, int64_t K, int64_t N, int64_t M) {
+  const size_t gu = (2 * static_cast<size_t>(M) * static_cast<size_t>(N) * sizeof(float) + 255) & ~size_t{255};
+  return gu + qk::gemm_workspace_bytes(M, K, type, N);
+}
+
+int run_ffn_gemm(const float* x, const void* gate, const void* up, int type, int64_t K, int64_t N,
+                 float* h, int64_t M, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const size_t need = ffn_gemm_bytes(type, K, N, M);
+  void* scratch = workspace;
+  if (scratch) {
+    if (workspace_bytes < need) return fail(QK_ERR_INVALID_ARGUMENT, "ffn workspace too small");
+    if (reinterpret_cast<uintptr_t>(scratch) % 16 != 0)
+      return fail(QK_ERR_INVALID_ARGUMENT, "ffn workspace must be 16-byte aligned");
+  } else {
+    const hipError_t error = hipMallocAsync(&scratch, need, stream);
+    if (error != hipSuccess) return hip_fail(error, "ffn scratch allocation failed");
+  }
+  float* gu = static_cast<float*>(scratch);
+  const size_t gu_bytes = need - qk::gemm_workspace_bytes(M, K, type, N);
+  const qk_segment segments[2] = {{gate, type, N, gu}, {up, type, N, gu + M * N}};
+  int status = run_gemm(x, M, K, segments, 2, static_cast<char*>(scratch) + gu_bytes, need - gu_bytes,
+                        stream);
+  if (status == QK_OK) {
+    const hipError_t error = qk::launch_silu_multiply(gu, gu + M * N, h, M * N, stream);
+    if (error != hipSuccess) status = hip_fail(error, "silu_multiply launch failed");
+  }
+  if (!workspace) (void)hipFreeAsync(scratch, stream);
+  return status;
+}
+
+int ffn_gate_up(const float* x, const void* gate, const void* up, int type, int64_t K, int64_t N,
+                float* h, int64_t M, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const int status = validate_matmul(type, K, N, M);
+  if (status != QK_OK) return status;
+  if (M == 0) return QK_OK;
+  if (!x || !gate || !up || !h) return fail(QK_ERR_INVALID_ARGUMENT, "ffn pointers must be non-null");
+  for (const void* w : {gate, up}) {
+    const int status = validate_weight_pointer(w, type);
+    if (status != QK_OK) return status;
+  }
+  if (M > qk::kGemvMaxRows)
+    return run_ffn_gemm(x, gate, up, type, K, N, h, M, workspace, workspace_bytes, stream);
+  qk::MatvecParams p = params_for(x, nullptr);
+  p.nseg = 2;
+  p.h = h;
+  p.seg[0] = {static_cast<const uint8_t*>(gate), nullptr, static_cast<int32_t>(N), type, 0, 0};
+  p.seg[1] = {static_cast<const uint8_t*>(up), nullptr, static_cast<int32_t>(N), type, 0, 0};
+  return run_matvec(p, M, K, 1, stream);
+}
+
+// Largest workspace of the segments (they run one after another on one prep).
+size_t segments_gemm_bytes(int64_t M, int64_t K, const qk_segment* segments, int count) {
+  size_t need = 0;
+  for (int j = 0; j < count; ++j)
+    need = std::max(need, qk::gemm_workspace_bytes(M, K, segments[j].type, segments[j].N));
+  return need;
+}
+
+int matmul_segments(const float* x, int64_t M, int64_t K, const qk_segment* segments, int count,
+                    void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (count < 1 || count > qk::kMaxSegments || !segments)
     return fail(QK_ERR_INVALID_ARGUMENT, "segment count must be in [1, 4]");
   if (K <= 0 || K % 256 != 0) return fail(QK_ERR_INVALID_ARGUMENT, "Invalid matmul weight dimensions");
@@ -285,61 +349,58 @@ int qk_matmul_segments(const float* x, int64_t M, int64_t K, const qk_segment* s
   for (int j = 0; j < count; ++j)
     if (!segments[j].w || !segments[j].y)
       return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
-  if (M > qk::kGemvMaxRows) return run_gemm(x, M, K, segments, count, nullptr, 0, as_stream(stream));
+  if (M > qk::kGemvMaxRows) return run_gemm(x, M, K, segments, count, workspace, workspace_bytes, stream);
   qk::MatvecParams p = params_for(x, nullptr);
   p.nseg = count;
   for (int j = 0; j < count; ++j) {
-    if (!segments[j].w || !segments[j].y)
-      return fail(QK_ERR_INVALID_ARGUMENT, "matmul pointers must be non-null");
     const int status = validate_weight_pointer(segments[j].w, segments[j].type);
     if (status != QK_OK) return status;
     p.seg[j] = {static_cast<const uint8_t*>(segments[j].w), segments[j].y,
                 static_cast<int32_t>(segments[j].N), segments[j].type, 0, 0};
   }
-  return run_matvec(p, M, K, 0, as_stream(stream));
-}
-
-namespace {
-
-// Prefill FFN (M > 8): gate and up through the GEMM (one launch for both
-// where no split K is needed) into stream-ordered scratch, then
-// SiLU(gate) * up into h.
-int run_ffn_gemm(const float* x, const void* gate, const void* up, int type, int64_t K, int64_t N,
-                 float* h, int64_t M, hipStream_t stream) {
-  float* gu = nullptr;
-  hipError_t error = hipMallocAsync(reinterpret_cast<void**>(&gu),
-                                    2 * static_cast<size_t>(M) * static_cast<size_t>(N) * sizeof(float),
-                                    stream);
-  if (error != hipSuccess) return hip_fail(error, "ffn scratch allocation failed");
-  const qk_segment segments[2] = {{gate, type, N, gu}, {up, type, N, gu + M * N}};
-  int status = run_gemm(x, M, K, segments, 2, nullptr, 0, stream);
-  if (status == QK_OK) {
-    error = qk::launch_silu_multiply(gu, gu + M * N, h, M * N, stream);
-    if (error != hipSuccess) status = hip_fail(error, "silu_multiply launch failed");
-  }
-  (void)hipFreeAsync(gu, stream);
-  return status;
+  return run_matvec(p, M, K, 0, stream);
 }
 
 }  // namespace
 
+int qk_matmul_segments(const float* x, int64_t M, int64_t K, const qk_segment* segments, int count,
+                       qk_stream_t stream) {
+  return matmul_segments(x, M, K, segments, count, nullptr, 0, as_stream(stream));
+}
+
+size_t qk_matmul_segments_workspace_size(int64_t M, int64_t K, const qk_segment* segments, int count) {
+  if (!segments || count < 1 || count > qk::kMaxSegments || K <= 0 || K % 256 != 0 || K > kMaxK ||
+      M <= qk::kGemvMaxRows)
+    return 0;
+  for (int j = 0; j < count; ++j)
+    if (!supported_type(segments[j].type) || segments[j].N <= 0) return 0;
+  return segments_gemm_bytes(M, K, segments, count);
+}
+
+int qk_matmul_segments_ws(const float* x, int64_t M, int64_t K, const qk_segment* segments, int count,
+                          void* workspace, size_t workspace_bytes, qk_stream_t stream) {
+  if (M > qk::kGemvMaxRows && !workspace)
+    return fail(QK_ERR_INVALID_ARGUMENT, "matmul workspace must be non-null");
+  return matmul_segments(x, M, K, segments, count, workspace, workspace_bytes, as_stream(stream));
+}
+
 int qk_ffn_gate_up(const float* x, const void* gate, const void* up, int type, int64_t K, int64_t N,
                    float* h, int64_t M, qk_stream_t stream) {
-  const int status = validate_matmul(type, K, N, M);
-  if (status != QK_OK) return status;
-  if (M == 0) return QK_OK;
-  if (!x || !gate || !up || !h) return fail(QK_ERR_INVALID_ARGUMENT, "ffn pointers must be non-null");
-  for (const void* w : {gate, up}) {
-    const int status = validate_weight_pointer(w, type);
-    if (status != QK_OK) return status;
-  }
-  if (M > qk::kGemvMaxRows) return run_ffn_gemm(x, gate, up, type, K, N, h, M, as_stream(stream));
-  qk::MatvecParams p = params_for(x, nullptr);
-  p.nseg = 2;
-  p.h = h;
-  p.seg[0] = {static_cast<const uint8_t*>(gate), nullptr, static_cast<int32_t>(N), type, 0, 0};
-  p.seg[1] = {static_cast<const uint8_t*>(up), nullptr, static_cast<int32_t>(N), type, 0, 0};
-  return run_matvec(p, M, K, 1, as_stream(stream));
+  return ffn_gate_up(x, gate, up, type, K, N, h, M, nullptr, 0, as_stream(stream));
+}
+
+size_t qk_ffn_gate_up_workspace_size(int type, int64_t K, int64_t N, int64_t M) {
+  if (!supported_type(type) || K <= 0 || K % 256 != 0 || K > kMaxK || N <= 0 ||
+      N > (int64_t{1} << 31) - 64 || M <= qk::kGemvMaxRows)
+    return 0;
+  return ffn_gemm_bytes(type, K, N, M);
+}
+
+int qk_ffn_gate_up_ws(const float* x, const void* gate, const void* up, int type, int64_t K, int64_t N,
+                      float* h, int64_t M, void* workspace, size_t workspace_bytes, qk_stream_t stream) {
+  if (M > qk::kGemvMaxRows && !workspace)
+    return fail(QK_ERR_INVALID_ARGUMENT, "ffn workspace must be non-null");
+  return ffn_gate_up(x, gate, up, type, K, N, h, M, workspace, workspace_bytes, as_stream(stream));
 }
 
 int qk_ffn_gate_up_norm(const float* x, const float* norm, float eps, const void* gate, const void* up,

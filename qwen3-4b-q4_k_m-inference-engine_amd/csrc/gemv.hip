@@ -98,15 +98,11 @@ int matvec_rows_per_launch(int64_t K) {
 }
 
 hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
-  // M = 1 shapes whose per-CU share fits in LDS take the whole-share kernel
-  // (gemv_stream.hip); QK_NO_STREAM_MATVEC builds keep every shape here.
-#ifndef QK_NO_STREAM_MATVEC
+  // Shapes whose per-CU share fits in LDS take the whole-share kernel
+  // (gemv_stream.hip).
   bool launched = false;
   hipError_t e = launch_stream_matvec(p, mode, stream, launched);
   if (e != hipSuccess || launched) return e;
-#else
-  hipError_t e = hipSuccess;
-#endif
   DeviceFacts dev;
   e = device_facts(dev);
   if (e != hipSuccess) return e;
@@ -156,9 +152,6 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
   int lpr = 64;
   int64_t best = INT64_MAX;
   for (int cand : {8, 16, 32, 64}) {
-#ifdef QK_MATVEC_FORCE_LPR
-    if (cand != QK_MATVEC_FORCE_LPR) continue;
-#endif
     int64_t cost = 0;
     if (rows4) cost = std::max(cost, wave_iterations(rows4, wg4 * waves, cand, p.S, mode) * kQ4KBytes);
     if (rows6)

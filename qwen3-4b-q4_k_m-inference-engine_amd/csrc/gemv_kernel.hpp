@@ -31,34 +31,22 @@
 namespace qk {
 
 // Waves per workgroup, iterations per chunk (Q4_K, Q6_K) and activation
-// tasks staged per quantiser lane. The defaults are the values measured best
-// on the Qwen3-4B decode sweep; the macros exist for tuning builds.
-#ifndef QK_MATVEC_WAVES_MT
-#define QK_MATVEC_WAVES_MT 8  // M > 1: several accumulators per lane need 256 VGPRs
-#endif
-#ifndef QK_MATVEC_U4
-#define QK_MATVEC_U4 2
-#endif
-#ifndef QK_MATVEC_U6
-#define QK_MATVEC_U6 1
-#endif
-#ifndef QK_MATVEC_XSTAGED
-#define QK_MATVEC_XSTAGED 2
-#endif
-// M = 1 on this kernel means a shape too large for the whole-share kernel
-// (the lm_head: one long stream per wave), measured faster with 8 waves
-// each two Q6_K iterations deep (196 VGPRs; 16 waves that deep spill) than
-// with 16 waves one iteration deep.
-#ifndef QK_MATVEC_WAVES_M1
-#define QK_MATVEC_WAVES_M1 8
-#endif
-#ifndef QK_MATVEC_U6_M1
-#define QK_MATVEC_U6_M1 2
-#endif
+// tasks staged per quantiser lane: the values measured best on the Qwen3-4B
+// decode sweep. M > 1: 8 waves, several accumulators per lane in up to 256
+// VGPRs. M = 1 on this kernel means a shape too large for the whole-share
+// kernel (the lm_head: one long stream per wave), measured faster with 8
+// waves each two Q6_K iterations deep (196 VGPRs; 16 waves that deep spill)
+// than with 16 waves one iteration deep.
+constexpr int kMatvecWavesMt = 8;
+constexpr int kMatvecU4 = 2;
+constexpr int kMatvecU6 = 1;
+constexpr int kMatvecXStaged = 2;
+constexpr int kMatvecWavesM1 = 8;
+constexpr int kMatvecU6M1 = 2;
 // Waves per workgroup for MT activation rows.
 template <int MT>
 constexpr int matvec_waves() {
-  return MT == 1 ? QK_MATVEC_WAVES_M1 : QK_MATVEC_WAVES_MT;
+  return MT == 1 ? kMatvecWavesM1 : kMatvecWavesMt;
 }
 
 // Per-lane register image of one iteration's piece.
@@ -162,7 +150,7 @@ __device__ __forceinline__ void quantize_group(const float (&v)[8], lds_q8_block
 // while those are in flight. Global loads return in issue order per wave, so
 // the other waves' weight loads never wait behind activation loads. Tasks
 // beyond the staged ones (M > 1 with wide K) load and quantise afterwards.
-constexpr int kXStaged = QK_MATVEC_XSTAGED;
+constexpr int kXStaged = kMatvecXStaged;
 
 template <int MT>
 struct XStage {
@@ -504,8 +492,8 @@ template <int MT, int LPR, int MODE, int TYPE, bool Q8IN>
 __global__ __launch_bounds__((64 * matvec_waves<MT>())) void matvec_kernel(const MatvecParams p) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
   lds_q8_block* xq = (lds_q8_block*)(lds_raw);
-  constexpr int U4 = QK_MATVEC_U4;
-  constexpr int U6 = MT == 1 ? QK_MATVEC_U6_M1 : QK_MATVEC_U6;
+  constexpr int U4 = kMatvecU4;
+  constexpr int U6 = MT == 1 ? kMatvecU6M1 : kMatvecU6;
 
   MatvecArgs a;
   a.x = p.x;

@@ -5,6 +5,7 @@ No compute call is made: every call here returns before any HIP call."""
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 import re
 import subprocess
@@ -173,3 +174,48 @@ def test_rms_norm_and_residual_add_validation(qk):
     assert lib.qk_residual_add(None, None, 0, None) == 0
     assert lib.qk_residual_add(8, 8, -1, None) == 1
     assert lib.qk_residual_add(None, 8, 5, None) == 1
+
+
+def _sanitized_run(tmp_path, name, sources, extra):
+    exe = tmp_path / name
+    cmd = ["g++", "-std=c++20", "-g", "-O1", "-fno-omit-frame-pointer",
+           "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined",
+           "-I", str(ROOT / "include"), "-I", str(ROOT / "oracle"), *extra, *map(str, sources),
+           "-o", str(exe)]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    print(res.stdout[-3000:], res.stderr[-3000:])
+    assert res.returncode == 0, "sanitizer build failed"
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300, env=env)
+    print(res.stdout[-3000:], res.stderr[-3000:])
+    assert res.returncode == 0
+
+
+def test_host_layer_under_address_and_ub_sanitizers(tmp_path):
+    """The host layer (host/*.cpp: GGUF reader, Weight, DeviceBuffer, Kernels
+    validation, EmbedLookup) and its CPU tests built with -fsanitize=address,
+    undefined and run: no device call is made, libqk_hip.so only validates."""
+    build = ROOT / "qwen3-4b-q4_k_m-inference-engine_amd" / "_build"
+    assert (build / "libqk_hip.so").exists(), "build the package first"
+    host = sorted((ROOT / "qwen3-4b-q4_k_m-inference-engine_amd" / "host").glob("*.cpp"))
+    _sanitized_run(tmp_path, "host_tests_asan", host + [ROOT / "tests" / "cpp" / "host_tests.cpp"],
+                   ["-L", str(build), "-lqk_hip", f"-Wl,-rpath,{build}"])
+
+
+def test_oracle_under_address_and_ub_sanitizers(tmp_path):
+    """oracle/qk_oracle.c and a self-check driver of every function built with
+    -fsanitize=address,undefined (as C, -ffp-contract=off) and run."""
+    exe = tmp_path / "oracle_asan"
+    cmd = ["gcc", "-std=c11", "-g", "-O1", "-fno-omit-frame-pointer", "-ffp-contract=off", "-fopenmp",
+           "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-I", str(ROOT / "oracle"),
+           str(ROOT / "oracle" / "qk_oracle.c"), str(ROOT / "tests" / "cpp" / "oracle_selfcheck.c"),
+           "-lm", "-o", str(exe)]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    print(res.stdout[-3000:], res.stderr[-3000:])
+    assert res.returncode == 0, "sanitizer build failed"
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1", OMP_NUM_THREADS="2")
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300, env=env)
+    print(res.stdout[-3000:], res.stderr[-3000:])
+    assert res.returncode == 0 and "all checks passed" in res.stdout

@@ -246,3 +246,51 @@ def test_prefill_graph_replay_with_workspace(gpu, oracle):
         stream.synchronize()
     graph.destroy()
     stream.destroy()
+
+
+@pytest.mark.parametrize("qtype,K,N,M", [(Q4, 2560, 9728, 64), (Q6, 9728, 2560, 40)])
+def test_ffn_gate_up_workspace_variant_and_deep_k(gpu, oracle, qtype, K, N, M):
+    """qk_ffn_gate_up_ws equals qk_ffn_gate_up bit for bit; the deep-K shape
+    (K = 9728, N = 2560) takes the split-K GEMM for gate and up in separate
+    launches, checked against the oracle."""
+    gate = make_weight(gpu, qtype, N, K, SEED + 60)
+    up = make_weight(gpu, qtype, N, K, SEED + 61)
+    x = oracle.synth_normal(M * K, SEED + 62)
+    xd = gpu.DeviceBuffer.from_array(x)
+    h1, h2 = gpu.DeviceBuffer(4 * M * N), gpu.DeviceBuffer(4 * M * N)
+    gpu.ffn_gate_up(xd, gate, up, qtype, K, N, h1, M)
+    need = gpu.ffn_gate_up_workspace_size(qtype, K, N, M)
+    assert need >= 2 * M * N * 4 + gpu.matmul_workspace_size(qtype, K, N, M)
+    ws = gpu.DeviceBuffer(need)
+    gpu.ffn_gate_up_ws(xd, gate, up, qtype, K, N, h2, M, ws, need)
+    gpu.synchronize()
+    a, b = h1.download(np.float32), h2.download(np.float32)
+    assert np.array_equal(a, b)
+    g = oracle.reference_product(x, gate.download(np.uint8), qtype, K, N)
+    u = oracle.reference_product(x, up.download(np.uint8), qtype, K, N)
+    with np.errstate(over="ignore"):
+        ref = (g / (1.0 + np.exp(-g))) * u
+    err = oracle.row_norm_error(a.reshape(M, N), ref)
+    print(f"[case] ffn prefill type={qtype} K={K} N={N} M={M} error {err:.3e}", flush=True)
+    assert err <= 1e-5
+    assert gpu.load().qk_ffn_gate_up_ws(xd.ptr, gate.ptr, up.ptr, qtype, K, N, h2.ptr, M, ws.ptr,
+                                        need - 256, None) == 1
+
+
+def test_segments_workspace_variant(gpu, oracle):
+    """qk_matmul_segments_ws (q/k/v at M = 40) equals qk_matmul_segments bit for bit."""
+    K, M = 2560, 40
+    shapes = [(Q4, 4096), (Q4, 1024), (Q6, 1024)]
+    ws_ = [make_weight(gpu, q, N, K, SEED + 70 + i) for i, (q, N) in enumerate(shapes)]
+    xd = gpu.DeviceBuffer.from_array(oracle.synth_normal(M * K, SEED + 73))
+    y1 = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes]
+    y2 = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes]
+    gpu.matmul_segments(xd, M, K, [(w, q, N, y) for w, (q, N), y in zip(ws_, shapes, y1)])
+    segs = [(w, q, N, y) for w, (q, N), y in zip(ws_, shapes, y2)]
+    need = gpu.matmul_segments_workspace_size(M, K, segs)
+    assert need == max(gpu.matmul_workspace_size(q, K, N, M) for q, N in shapes)
+    work = gpu.DeviceBuffer(need)
+    gpu.matmul_segments_ws(xd, M, K, segs, work, need)
+    gpu.synchronize()
+    for a, b in zip(y1, y2):
+        assert np.array_equal(a.download(np.float32), b.download(np.float32))
