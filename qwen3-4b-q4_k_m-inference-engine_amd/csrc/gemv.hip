@@ -103,6 +103,9 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
   bool launched = false;
   hipError_t e = launch_stream_matvec(p, mode, stream, launched);
   if (e != hipSuccess || launched) return e;
+  // Larger M = 1 shapes and the lm_head + argmax: the multi-pass form (gemv_pass.hip).
+  e = launch_pass_matvec(p, mode, stream, launched);
+  if (e != hipSuccess || launched) return e;
   DeviceFacts dev;
   e = device_facts(dev);
   if (e != hipSuccess) return e;

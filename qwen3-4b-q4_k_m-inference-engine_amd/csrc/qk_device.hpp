@@ -241,26 +241,35 @@ struct Q6KCodes {
   float d;
 };
 
+// (a & mask) | (b & ~mask) in one instruction (the compiler's own pattern
+// match misses it once known-bits analysis has narrowed b's mask).
+__device__ __forceinline__ uint32_t bit_insert(uint32_t mask, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
+  return r;
+}
+
 // q = ((ql >> 4*(g/2)) & 15) | ((qh >> 2g) & 3) << 4 (src/cuda/matmul.cu:71-79).
+// The realignment of a 2-byte-aligned superblock (shift 16) rides in the
+// funnel shifts: la = the aligned ql dword (low nibbles: group r), lb = it
+// shifted down by 4 (high nibbles: group r+2), qs = the aligned qh dword
+// shifted down by 2r and masked to bits 0-1 (group r) and 4-5 (group r+2) of
+// every byte; two bit-field inserts form the codes. Bits shifted in from the
+// next dword land only in masked-off positions. 7 VALU per 8 codes.
 __device__ __forceinline__ Q6KCodes unpack_q6k_piece(const Q6KPiece& w, uint32_t p) {
   const uint32_t r = p & 1u;
-  const uint32_t sh = w.shift;
-  auto realign = [sh](uint32_t hi, uint32_t lo) { return __builtin_amdgcn_alignbit(hi, lo, sh); };
-  const uint32_t l[8] = {realign(w.l0.y, w.l0.x), realign(w.l0.z, w.l0.y), realign(w.l0.w, w.l0.z),
-                         realign(w.l1.x, w.l0.w), realign(w.l1.y, w.l1.x), realign(w.l1.z, w.l1.y),
-                         realign(w.l1.w, w.l1.z), realign(w.l2, w.l1.w)};
-  const uint32_t q[8] = {realign(w.h0.y, w.h0.x), realign(w.h0.z, w.h0.y), realign(w.h0.w, w.h0.z),
-                         realign(w.h1.x, w.h0.w), realign(w.h1.y, w.h1.x), realign(w.h1.z, w.h1.y),
-                         realign(w.h1.w, w.h1.z), realign(w.h2, w.h1.w)};
-  // rotate so bits (2g, 2g+1) of every qh byte land on bits 4 and 5
-  const uint32_t rot_a = (2u * r - 4u) & 31u;  // g = r
-  const uint32_t rot_b = 2u * r;               // g = r + 2: (2(r+2) - 4)
-  constexpr uint32_t kLo = 0x0F0F0F0Fu, kHi = 0x30303030u;
+  const uint32_t sh = w.shift;  // 0 or 16
+  const uint32_t l[9] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w, w.l1.x, w.l1.y, w.l1.z, w.l1.w, w.l2};
+  const uint32_t q[9] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w, w.h2};
+  constexpr uint32_t kLo = 0x0F0F0F0Fu, kFields = 0x33333333u;
   Q6KCodes c;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    c.a[i] = (l[i] & kLo) | (__builtin_amdgcn_alignbit(q[i], q[i], rot_a) & kHi);
-    c.b[i] = ((l[i] >> 4) & kLo) | (__builtin_amdgcn_alignbit(q[i], q[i], rot_b) & kHi);
+    const uint32_t la = __builtin_amdgcn_alignbit(l[i + 1], l[i], sh);
+    const uint32_t lb = __builtin_amdgcn_alignbit(l[i + 1], l[i], sh + 4u);
+    const uint32_t qs = __builtin_amdgcn_alignbit(q[i + 1], q[i], sh + 2u * r) & kFields;
+    c.a[i] = bit_insert(kLo, la, qs << 4);
+    c.b[i] = bit_insert(kLo, lb, qs);
   }
   c.sc = (w.sc_a & 0xFFFFu) | (w.sc_b << 16);
   c.d = half_bits_to_float(w.d_bits);

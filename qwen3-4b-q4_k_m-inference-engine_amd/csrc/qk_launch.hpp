@@ -65,6 +65,11 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream);
 // otherwise nothing is enqueued and launch_matvec uses the streaming kernel.
 hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
 
+// The multi-pass whole-share mat-vec (gemv_pass.hip): M = 1, one Q4_K or Q6_K
+// matrix, modes 0 and 2, rows up to kPassMaxJ KB; launched (and `launched`
+// set) when it takes the shape.
+hipError_t launch_pass_matvec(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
+
 // Compute units and LDS bytes per workgroup of the current device (cached).
 hipError_t device_limits(int& cus, int& max_lds);
 // Sets a kernel's dynamic LDS limit to `lds` bytes (once per kernel and size).

@@ -190,6 +190,22 @@ def test_matmul_m1_qwen3_shapes(gpu, oracle, name):
     assert_parity(oracle, got, ref)
 
 
+@pytest.mark.parametrize("qtype,K,N", [(Q6, 2560, 20001), (Q4, 2560, 40003), (Q6, 2816, 20001),
+                                       (Q4, 9728, 17000), (Q6, 256, 200003)])
+def test_matmul_m1_multipass_shapes(gpu, oracle, qtype, K, N):
+    """M = 1 shapes whose per-CU share exceeds LDS take the multi-pass kernel
+    (passes of whole rows per wave): ragged matrix ends (N * row bytes not a
+    multiple of 16), Q6_K rows of an odd superblock count (2-byte aligned),
+    one-row passes (K = 9728 Q4_K) and many-row passes (K = 256)."""
+    w = make_weight(gpu, oracle, qtype, N, K, SEED + 500 + N + K)
+    x = oracle.synth_normal(K, SEED + 8)
+    got = run_matmul(gpu, w, qtype, K, N, x, 1)
+    print(f"[case] type={qtype} K={K} N={N} M=1 launch {gpu.last_launch()}", flush=True)
+    assert gpu.last_launch().startswith("pass_matvec_kernel")
+    ref = oracle.reference_product(x, w.download(np.uint8), qtype, K, N)
+    assert_parity(oracle, got, ref)
+
+
 _BATCH_WEIGHTS: dict = {}
 
 
