@@ -60,7 +60,8 @@ hipError_t launch_ffn_fused(const FfnArgs& a, hipStream_t stream, bool& launched
   if (jg == 0 || jd == 0 || (a.down_type == QK_TYPE_Q6_K && pd == 0) || jg + jd > 14) return hipSuccess;
   const int64_t q8 = static_cast<int64_t>(sizeof(qk_q8_block));
   const int64_t lds_a = S * 8 * q8 + kStreamWaves * jg * 1024 + 2 * max_sb * 4 + 4 * kStreamWaves;
-  const int64_t lds_b = Sd * 8 * q8 + kStreamWaves * jd * 1024 + max_sbd * 4;
+  const int64_t lds_b = ffn_down_offset(static_cast<int>(S), jg, static_cast<int>(max_sb), static_cast<int>(Sd), jd) +
+                        kStreamWaves * jd * 1024 + max_sbd * 4;
   const int64_t lds = std::max(lds_a, lds_b);
   if (lds > max_lds) return hipSuccess;
   const bool norm = a.norm != nullptr;

@@ -11,12 +11,14 @@
 //      whole-share product of its range of down rows.
 // The down weights do not depend on h: waves 0..14 issue their share of them
 // (16-byte loads of a contiguous superblock run, as for gate/up) during phase
-// A, once half of their gate/up chunks have arrived, so they stream while
-// phase A computes. Wave 15 forms phase A's row totals, stores h and runs the
-// grid barrier; its down "loads" re-read one chunk (every wave issues the same
-// loads, so the compiler's wait counts stay exact), and since gfx950 counts
-// stores and loads in one counter, the wait for its h stores to complete does
-// not include the real down stream. For a Q6_K down, while the barrier is
+// A, once their gate/up chunks are in LDS, so they stream while phase A
+// computes. (Issued after phase A's pieces instead, they were still being
+// issued when wave 15 stored h, and its stores queued behind them: +1.4 us.)
+// Wave 15 forms phase A's row totals, stores h and runs the grid barrier; its
+// down "loads" re-read one chunk (every wave issues the same loads, so the
+// compiler's wait counts stay exact), and since gfx950 counts stores and loads
+// in one counter, the wait for its h stores to complete does not include the
+// real down stream. For a Q6_K down, while the barrier is
 // pending the other waves move their chunks to LDS and unpack their pieces
 // into int8 codes in registers, so that after it only the integer dots with h
 // remain (done after the barrier, the unpacking measured ~3 us of VALU per CU
@@ -56,6 +58,19 @@ static_assert((3 + 2 * kSyncGroups) * kSyncLine * 4 <= kFfnSyncBytes, "barrier l
 
 constexpr int kFfnHWaves = 1;  // the last wave: phase A's row totals, the h stores, the barrier
 
+// Byte offset of phase B's down region: right after the Q8 of h, unless that
+// would overlap phase A's superblock sums (and norm partials), which the h
+// wave may still be reading while the other waves move their down chunks to
+// LDS; then right after those sums. (The Q8 of h itself is written after the
+// barrier, when every wave is past phase A.)
+__host__ __device__ constexpr int ffn_down_offset(int S, int JG, int max_sb, int Sd, int JD) {
+  const int q8 = 48;  // sizeof(qk_q8_block)
+  const int sums_a = S * 8 * q8 + kStreamWaves * JG * 1024;
+  const int sums_a_end = sums_a + 2 * max_sb * 4 + 4 * kStreamWaves;
+  const int after_h = Sd * 8 * q8;
+  return after_h + kStreamWaves * JD * 1024 <= sums_a ? after_h : sums_a_end;
+}
+
 struct FfnParams {
   const float* x;         // [K]
   const float* norm;      // RMSNorm scale [K] (NORM kernels)
@@ -80,6 +95,14 @@ __device__ __forceinline__ uint32_t load_agent(const global_u32* p) {
 }
 __device__ __forceinline__ void store_agent(global_u32* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The epoch of the last barrier on this workspace, as workgroup b's group
+// release word holds it (every release writes all 8 of them): 256 workgroups
+// reading one word at launch serialise on it, 8 words spread them.
+__device__ __forceinline__ uint32_t last_epoch_of(const uint32_t* sync) {
+  const int g = static_cast<int>(blockIdx.x) & (kSyncGroups - 1);
+  return load_agent((const global_u32*)(sync) + kSyncRelease0 + g * kSyncLine);
 }
 
 // Thread 0 of a workgroup, once its workgroup's h stores are complete.
@@ -171,7 +194,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
   // which misses every cache; unconditional (a branch around it made the
   // compiler wait for it at the branch's end), and the increment waits for
   // the barrier.
-  const uint32_t last_epoch = load_agent((const global_u32*)(p.sync) + kSyncEpoch);
+  const uint32_t last_epoch = last_epoch_of(p.sync);
 
   const int wg = static_cast<int>(blockIdx.x);
   int r0 = wg * p.per + min(wg, p.rem);
@@ -260,11 +283,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
   stream_consume<TG, JG, 1, false, NORM, true, kHWave, kFfnHWaves, JG - 1>(
       wsg, S, max_sb, r0, r1, nullptr, (global_f32*)(hout), xq, wlds, sums, out_scale, issue_down);
 
-  // LDS of phase B: Q8 of h, then the down regions of the waves (JD KB each),
-  // then the superblock sums; none of it overlaps phase A's sums, which wave
-  // 15 is still reading.
+  // LDS of phase B: Q8 of h, the down regions of the waves (JD KB each) at
+  // ffn_down_offset (clear of phase A's sums, which wave 15 may still be
+  // reading), then the superblock sums.
+  static_assert(sizeof(qk_q8_block) == 48, "Q8 block layout");
   lds_q8_block* hq = (lds_q8_block*)(lds_raw);
-  lds_u8* dlds = (lds_u8*)(lds_raw) + Sd * 8 * static_cast<int>(sizeof(qk_q8_block));
+  lds_u8* dlds = (lds_u8*)(lds_raw) + ffn_down_offset(S, JG, max_sb, Sd, JD);
   lds_f32* dsums = reinterpret_cast<lds_f32*>(dlds + kStreamWaves * JD * 1024);
   DownCodes<kEarly ? PD : 1> dc;
   const int npc = 4 * (wsd.sb_b - wsd.sb_a);

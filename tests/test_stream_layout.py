@@ -308,6 +308,15 @@ def _depth(sb, nbytes):
     return -(-(-(-(2 + sb * nbytes) // 16)) // 64)
 
 
+def ffn_down_offset(S, JG, max_sb, Sd, JD):
+    """ffn_fused.hpp ffn_down_offset: phase B's down region after the Q8 of h, or
+    after phase A's sums when it would overlap them."""
+    sums_a = S * 8 * 48 + WAVES * JG * 1024
+    sums_a_end = sums_a + 2 * max_sb * 4 + 4 * WAVES
+    after_h = Sd * 8 * 48
+    return after_h if after_h + WAVES * JD * 1024 <= sums_a else sums_a_end
+
+
 def ffn_launcher(K, N, down_type, gate_up_type=12):
     """(G, per, rem, dper, drem, max_sb, max_sbd, JG, JD, PD, lds) or None (two-launch path)."""
     if gate_up_type != 12 or K > MAX_K or N > MAX_K or K % 256 or N % 256:
@@ -326,7 +335,7 @@ def ffn_launcher(K, N, down_type, gate_up_type=12):
     if jg == 0 or jd == 0 or (down_type == 14 and (pd == 0 or (jd, pd) not in Q6_PAIRS)) or jg + jd > 14:
         return None
     lds_a = S * 8 * 48 + WAVES * jg * 1024 + 2 * max_sb * 4 + 4 * WAVES
-    lds_b = Sd * 8 * 48 + WAVES * jd * 1024 + max_sbd * 4
+    lds_b = ffn_down_offset(S, jg, max_sb, Sd, jd) + WAVES * jd * 1024 + max_sbd * 4
     lds = max(lds_a, lds_b)
     if lds > MAX_LDS:
         return None
@@ -405,7 +414,12 @@ def check_ffn(K, N, down_type, bases):
     # LDS: phase A (Q8 of x, wave regions, both parts' sums, norm partials);
     # phase B (Q8 of h, wave regions, sums) reuse the same bytes
     assert S * 8 * 48 + WAVES * JG * 1024 + 2 * max_sb * 4 + 4 * WAVES <= lds <= MAX_LDS
-    assert Sd * 8 * 48 + WAVES * JD * 1024 + max_sbd * 4 <= lds
+    dl = ffn_down_offset(S, JG, max_sb, Sd, JD)
+    assert dl >= Sd * 8 * 48 and dl + WAVES * JD * 1024 + max_sbd * 4 <= lds
+    # the down regions, written while the h wave still reads phase A's sums
+    # (and norm partials), do not overlap them
+    sums_a, sums_a_end = S * 8 * 48 + WAVES * JG * 1024, S * 8 * 48 + WAVES * JG * 1024 + 2 * max_sb * 4 + 4 * WAVES
+    assert dl + WAVES * JD * 1024 <= sums_a or dl >= sums_a_end
     # barrier words: 3 + 2 x 8 lines of 256 bytes
     assert (3 + 2 * 8) * 256 <= SYNC_BYTES
     return True
