@@ -333,7 +333,8 @@ def measure_configs(qk, sweep: DecodeSweep, stream):
     ms = time_graph(qk, graph, stream, 2, 10)
     graph.destroy()
     out["4_decode_sweep_m8"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(8e3 / ms, 1),
-                                "GB/s": round(sweep8.bytes_per_step() / (ms * 1e6), 1)}
+                                "GB/s": round(sweep8.bytes_per_step() / (ms * 1e6), 1),
+                                "kernels": kernel_roofline(qk, sweep8, stream)}
     return out
 
 

@@ -62,7 +62,7 @@ __device__ __forceinline__ void prep_group(const f32x4 a, const f32x4 b, float u
   if (bmax >= 0x1p-64f && bmax <= 0x1p64f) {
     const float r = refined_rcp(bmax);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) code[i] = static_cast<float>(round_code(markstein_div(v[i], bmax, r) * 127.0f));
+    for (int i = 0; i < 8; ++i) code[i] = static_cast<float>(q8_code(v[i], bmax, r));
     scale = markstein_div(bmax, 127.0f, 1.0f / 127.0f);
   } else {
 #pragma unroll

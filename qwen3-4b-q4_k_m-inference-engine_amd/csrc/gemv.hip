@@ -98,10 +98,14 @@ int matvec_rows_per_launch(int64_t K) {
 }
 
 hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
+  // M = 2..8 with fp32 activations: the batched mat-vec on the matrix cores
+  // (bmv.hip).
+  bool launched = false;
+  hipError_t e = launch_bmv(p, mode, stream, launched);
+  if (e != hipSuccess || launched) return e;
   // Shapes whose per-CU share fits in LDS take the whole-share kernel
   // (gemv_stream.hip).
-  bool launched = false;
-  hipError_t e = launch_stream_matvec(p, mode, stream, launched);
+  e = launch_stream_matvec(p, mode, stream, launched);
   if (e != hipSuccess || launched) return e;
   // Larger M = 1 shapes and the lm_head + argmax: the multi-pass form (gemv_pass.hip).
   e = launch_pass_matvec(p, mode, stream, launched);

@@ -98,7 +98,17 @@ __device__ __forceinline__ int piece_block_step(int type) { return type == QK_TY
 // and round_code live in qk_device.hpp; tests/cpp/quant_arith_check.hip
 // repeats the exhaustive checks on the GPU.)
 
-__device__ __forceinline__ void quantize_group(const float (&v)[8], lds_q8_block* blk, uint32_t q) {
+// One quad lane's share of a 32-value block: its 8 codes packed in two dwords,
+// the block scale, and (from the quad's DPP sums) the sums of codes 0..15
+// (pair) and 16..31 (other) as seen by lane 0 of the quad. Every lane of the
+// quad must call it (the DPP exchanges read the neighbours).
+struct Q8Quarter {
+  uint32_t lo, hi;
+  float scale;
+  int pair, other;
+};
+
+__device__ __forceinline__ Q8Quarter quantize_quarter(const float (&v)[8]) {
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -112,7 +122,7 @@ __device__ __forceinline__ void quantize_group(const float (&v)[8], lds_q8_block
   if (usual) {
     const float r = refined_rcp(amax);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) code[i] = round_code(markstein_div(v[i], amax, r) * 127.0f);
+    for (int i = 0; i < 8; ++i) code[i] = q8_code(v[i], amax, r);
     scale = markstein_div(amax, 127.0f, 1.0f / 127.0f);
   } else if (amax == 0.0f) {
 #pragma unroll
@@ -131,15 +141,20 @@ __device__ __forceinline__ void quantize_group(const float (&v)[8], lds_q8_block
     hi |= (static_cast<uint32_t>(code[i + 4]) & 0xFFu) << (8 * i);
     sum += code[i] + code[i + 4];
   }
-  *reinterpret_cast<lds_u32x2*>(blk->codes + 8 * q) = u32x2{lo, hi};
   // lanes 0,1 of the quad hold codes 0..15, lanes 2,3 codes 16..31
   const int pair = sum + __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, false);
   const int other = __builtin_amdgcn_update_dpp(0, pair, 0x4E, 0xF, 0xF, false);
+  return Q8Quarter{lo, hi, scale, pair, other};
+}
+
+__device__ __forceinline__ void quantize_group(const float (&v)[8], lds_q8_block* blk, uint32_t q) {
+  const Q8Quarter r = quantize_quarter(v);
+  *reinterpret_cast<lds_u32x2*>(blk->codes + 8 * q) = u32x2{r.lo, r.hi};
   if (q == 0) {
-    blk->scale = scale;
-    blk->scaled_sum = scale * static_cast<float>(pair + other);
-    blk->neg32_sum_lo = -32 * pair;
-    blk->neg32_sum_hi = -32 * other;
+    blk->scale = r.scale;
+    blk->scaled_sum = r.scale * static_cast<float>(r.pair + r.other);
+    blk->neg32_sum_lo = -32 * r.pair;
+    blk->neg32_sum_hi = -32 * r.other;
   }
 }
 

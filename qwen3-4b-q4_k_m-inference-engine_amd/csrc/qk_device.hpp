@@ -115,7 +115,8 @@ struct XFrag {  // one Q8 activation block
 //  refined_rcp(a)        = RN(1/a): v_rcp_f32 plus one FMA refinement;
 //  markstein_div(x,b,r)  = RN(x/b) given r = RN(1/b) (Markstein's correction);
 //  round_code(t)         = roundf(t) for |t| <= 127, as a truncation of
-//                          t + copysign(0.49999997f, t).
+//                          t + copysign(0.49999997f, t);
+//  q8_code(x, amax, r)   = roundf(RN(x/amax) * 127) from the two above.
 // Each identity holds for every float in its range: tests/cpp/
 // quant_arith_check.hip checks them exhaustively on the GPU.
 __device__ __forceinline__ float refined_rcp(float a) {
@@ -127,6 +128,18 @@ __device__ __forceinline__ float markstein_div(float x, float b, float r) {
   return __builtin_fmaf(__builtin_fmaf(-q0, b, x), r, q0);
 }
 __device__ __forceinline__ int round_code(float t) {
+#pragma clang fp contract(off)
+  return static_cast<int>(t + __builtin_copysignf(0.49999997f, t));
+}
+
+// The Q8 code of x in a block with maximum amax, given r = RN(1/amax):
+// roundf(RN(RN(x/amax) * 127)), the reference's float formula. Contraction is
+// off: fused into one FMA, the product and the rounding add skip the rounding
+// of the product, and a quotient just below a half (x = 1, amax = 254:
+// 0.49999999814 -> RN 0.5 -> code 1) truncates to the code below.
+__device__ __forceinline__ int q8_code(float x, float amax, float r) {
+#pragma clang fp contract(off)
+  const float t = markstein_div(x, amax, r) * 127.0f;
   return static_cast<int>(t + __builtin_copysignf(0.49999997f, t));
 }
 

@@ -70,6 +70,11 @@ hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t str
 // set) when it takes the shape.
 hipError_t launch_pass_matvec(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
 
+// The batched mat-vec on the int8 matrix cores (bmv.hip): M = 2..8 rows of
+// fp32 activations, modes 0 and 1; launched (and `launched` set) when the
+// shape fits its LDS plan.
+hipError_t launch_bmv(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
+
 // Compute units and LDS bytes per workgroup of the current device (cached).
 hipError_t device_limits(int& cus, int& max_lds);
 // Sets a kernel's dynamic LDS limit to `lds` bytes (once per kernel and size).

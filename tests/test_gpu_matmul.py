@@ -441,16 +441,55 @@ def test_ffn_gate_up_norm_small_shapes(gpu, oracle, qtype, K, N, eps, xscale):
     assert err <= 1e-3
 
 
-def test_prologue_quantisation_matches_quantize_kernel(gpu, oracle):
-    """The in-kernel Q8 (reciprocal + correction) equals the IEEE-division quantize
-    kernel on wide-range data with many exact rounding ties."""
+def _quantiser_input(K, M):
+    """Wide-range activations (|x| from ~1e-13 to ~1e13) with blocks of exact
+    rounding ties ((k + 0.5)/127 * amax) and an all-zero block."""
     rng = np.random.default_rng(99)
-    K, M, N = 9728, 4, 64
     x = (rng.standard_normal(M * K) * np.exp(rng.uniform(-30, 30, M * K))).astype(np.float32)
-    # blocks whose values sit on (k+0.5)/127 * amax ties
     amax = np.float32(254.0)
     x[: 32 * 64] = np.tile(np.concatenate([[amax], (np.arange(31) * 2 + 1).astype(np.float32)]), 64)
     x[32 * 64: 32 * 65] = 0.0
+    return x
+
+
+def _one_hot_q4k(K):
+    """Q4_K [K x K]: row n holds weight 1 at position n and 0 elsewhere (d = 1,
+    every sub-block scale 1, every min 0), so row n of x . W^T is Q8(x)[n]."""
+    S = K // 256
+    template = np.frombuffer(pack_q4k(0x3C00, 0, [1] * 8, [0] * 8, [0] * 256), dtype=np.uint8)
+    w = np.tile(template, K * S).reshape(K, S, 144)
+    n = np.arange(K)
+    p = n % 256
+    w[n, n // 256, 16 + 32 * (p // 64) + p % 32] = np.where((p % 64) >= 32, 0x10, 0x01)
+    return w.reshape(-1)
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_prologue_quantisation_bitwise(gpu, oracle, M):
+    """The in-launch Q8 quantiser (reciprocal + Markstein correction; M = 1: the
+    whole-share kernel, M = 2..8: the matrix-core kernel) gives the reference's
+    round trip round(x/amax*127) * (amax/127) (src/cuda/matmul.cu:8-22,
+    src/tests/reference/MatmulReference.hpp:11-29) exactly at every
+    position: with the one-hot weights each output is one code times its block
+    scale, and every other term of its sums is an exact zero."""
+    K = 9728
+    x = _quantiser_input(K, M)
+    w = gpu.DeviceBuffer.from_array(_one_hot_q4k(K))
+    got = run_matmul(gpu, w, Q4, K, K, x, M)
+    print(f"[case] one-hot Q4_K K={K} M={M} launch {gpu.last_launch()}", flush=True)
+    ref = oracle.q8_roundtrip(x).reshape(M, K)
+    # equal as floats: the round trip's roundf gives -0.0 for small negative x
+    # where the integer codes give +0.0; every other value matches exactly
+    bad = np.nonzero(got != ref)
+    assert bad[0].size == 0, f"{bad[0].size} mismatches, first at (m, k) = ({bad[0][0]}, {bad[1][0]})"
+
+
+def test_quantize_kernel_matches_oracle_and_prologue(gpu, oracle):
+    """qk_quantize_q8 (IEEE division) gives the oracle's codes bit for bit, and
+    qk_matmul_q8 on them agrees with qk_matmul's in-launch quantisation (other
+    kernels, other summation orders)."""
+    K, M, N = 9728, 4, 64
+    x = _quantiser_input(K, M)
     w = make_weight(gpu, oracle, Q4, N, K, SEED + 800)
     xd = gpu.DeviceBuffer.from_array(x)
     y1 = gpu.DeviceBuffer(4 * M * N)
@@ -460,7 +499,9 @@ def test_prologue_quantisation_matches_quantize_kernel(gpu, oracle):
     y2 = gpu.DeviceBuffer(4 * M * N)
     gpu.matmul_q8(q8, w, Q4, K, N, y2, M)
     gpu.synchronize()
-    assert np.array_equal(y1.download(np.float32), y2.download(np.float32))
+    a = y1.download(np.float32).reshape(M, N)
+    b = y2.download(np.float32).reshape(M, N)
+    assert oracle.row_norm_error(a, b.astype(np.float64)) <= 1e-6
     codes, _ = oracle.quantize_q8(x)
     assert np.array_equal(q8.download(np.uint8).view(gpu.Q8_DTYPE)["codes"].ravel(), codes)
 

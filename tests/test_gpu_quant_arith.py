@@ -21,4 +21,4 @@ def test_quantiser_rounding_identities_exhaustive():
     res = subprocess.run([str(EXE)], capture_output=True, text=True, timeout=110)
     print(res.stdout, res.stderr)
     assert res.returncode == 0
-    assert res.stdout.count(": 0 mismatches") == 3
+    assert res.stdout.count(": 0 mismatches") == 4
