@@ -86,8 +86,9 @@ class DecodeSweep:
 
     def __init__(self, qk, M: int = 1, weights_of: "DecodeSweep | None" = None, fused_ffn: bool = True):
         self.qk, self.M = qk, M
-        # M = 1: the FFN block (gate, up, SiLU*up, down) in one launch (qk_ffn)
-        self.fused_ffn = fused_ffn and M == 1
+        # the FFN block through qk_ffn: M = 1 one launch (gate, up, SiLU*up,
+        # down); M = 2..8 gate/up, one Q8 of h into the workspace, down on it
+        self.fused_ffn = fused_ffn
         if weights_of is not None:  # same weights, other activation rows
             self.layers, self.lm_head = weights_of.layers, weights_of.lm_head
         else:

@@ -182,9 +182,11 @@ int qk_ffn_gate_up_norm(const float *x, const float *norm, float eps, const void
                         const void *up, int type, int64_t K, int64_t N, float *h, int64_t M,
                         qk_stream_t stream);
 
-/* Bytes of the workspace qk_ffn needs (its grid-barrier words). The caller
- * zero-fills it once before its first use; every call leaves it ready for the
- * next. Calls that may run concurrently need separate workspaces. */
+/* Bytes of the workspace qk_ffn needs: its grid-barrier words, then room for
+ * Q8(h) (160 KiB) and the RMSNorm rows (512 KiB) of the batched M = 2..8 block.
+ * The caller zero-fills it once before its first use; every call leaves it
+ * ready for the next. Calls that may run concurrently need separate
+ * workspaces. */
 size_t qk_ffn_workspace_size(void);
 
 /* The FFN block: h[M x N] = SiLU(Q8(x') . gate^T) * (Q8(x') . up^T) and
@@ -199,8 +201,12 @@ size_t qk_ffn_workspace_size(void);
  * loaded during phase 1. That launch needs every workgroup resident at once:
  * do not overlap it with other kernels on the device. Its barrier wait is
  * bounded: if it ever times out, the outputs of that call are invalid and
- * qk_ffn_workspace_check reports it. Other M or shapes: qk_ffn_gate_up(_norm)
- * then qk_matmul on the stream (allocating at M > 8 as they do). Validation
+ * qk_ffn_workspace_check reports it. M = 2..8 (when M*N/32 Q8 blocks fit in
+ * 160 KiB, M*K norm rows in 512 KiB and M rows of Q8(h) in one down launch):
+ * the norm into the workspace, qk_ffn_gate_up, h quantised once into the
+ * workspace, then the down mat-vec on those Q8 blocks; nothing is allocated.
+ * Other M or shapes: qk_ffn_gate_up(_norm) then qk_matmul on the stream
+ * (allocating at M > 8 as they do). Validation
  * as qk_matmul for both weights, plus the workspace (256-byte aligned, at
  * least qk_ffn_workspace_size bytes) and eps when norm is given. */
 int qk_ffn(const float *x, const float *norm, float eps, const void *gate, const void *up,

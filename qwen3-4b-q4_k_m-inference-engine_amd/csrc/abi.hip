@@ -446,7 +446,13 @@ int qk_ffn_gate_up_norm(const float* x, const float* norm, float eps, const void
   return result;
 }
 
-size_t qk_ffn_workspace_size(void) { return qk::ffn_sync_bytes(); }
+// qk_ffn workspace: the grid-barrier words, then (M = 2..8) Q8(h) and the
+// normalised rows, so the batched block allocates nothing and quantises h once
+// instead of in every CU of the down launch.
+constexpr size_t kFfnQ8Bytes = size_t{160} << 10;    // Q8 image of h, M*N/32 blocks
+constexpr size_t kFfnNormBytes = size_t{512} << 10;  // RMSNorm(x) rows, M*K floats
+
+size_t qk_ffn_workspace_size(void) { return qk::ffn_sync_bytes() + kFfnQ8Bytes + kFfnNormBytes; }
 
 int qk_ffn(const float* x, const float* norm, float eps, const void* gate, const void* up,
            int gate_up_type, const void* down, int down_type, int64_t K, int64_t N, float* h, float* y,
@@ -460,7 +466,7 @@ int qk_ffn(const float* x, const float* norm, float eps, const void* gate, const
     return fail(QK_ERR_INVALID_ARGUMENT, "RMSNorm requires a positive epsilon");
   if (!x || !gate || !up || !down || !h || !y)
     return fail(QK_ERR_INVALID_ARGUMENT, "ffn pointers must be non-null");
-  if (!workspace || workspace_bytes < qk::ffn_sync_bytes() ||
+  if (!workspace || workspace_bytes < qk_ffn_workspace_size() ||
       reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
     return fail(QK_ERR_INVALID_ARGUMENT,
                 "ffn workspace must be 256-byte aligned and hold qk_ffn_workspace_size() bytes");
@@ -477,6 +483,27 @@ int qk_ffn(const float* x, const float* norm, float eps, const void* gate, const
     const hipError_t error = qk::launch_ffn_fused(a, s, launched);
     if (error != hipSuccess) return hip_fail(error, "ffn launch failed");
     if (launched) return QK_OK;
+  }
+  // M = 2..8 with a full workspace: RMSNorm rows and Q8(h) in the workspace;
+  // gate/up, one quantisation of h, the down mat-vec on the Q8 blocks.
+  const size_t q8_bytes = static_cast<size_t>(M) * static_cast<size_t>(N / 32) * sizeof(qk_q8_block);
+  const size_t norm_bytes = norm ? static_cast<size_t>(M * K) * sizeof(float) : 0;
+  if (M >= 2 && M <= 8 && q8_bytes <= kFfnQ8Bytes && norm_bytes <= kFfnNormBytes &&
+      qk::matvec_rows_per_launch(N) >= M) {
+    char* base = static_cast<char*>(workspace) + qk::ffn_sync_bytes();
+    qk_q8_block* hq = reinterpret_cast<qk_q8_block*>(base);
+    const float* xin = x;
+    if (norm) {
+      float* normalized = reinterpret_cast<float*>(base + kFfnQ8Bytes);
+      const hipError_t error = qk::launch_rms_norm(x, norm, normalized, M, K, eps, s);
+      if (error != hipSuccess) return hip_fail(error, "RMSNorm launch failed");
+      xin = normalized;
+    }
+    status = qk_ffn_gate_up(xin, gate, up, gate_up_type, K, N, h, M, stream);
+    if (status != QK_OK) return status;
+    const hipError_t error = qk::launch_quantize_q8(h, M, N, hq, s);
+    if (error != hipSuccess) return hip_fail(error, "quantize launch failed");
+    return run_single(nullptr, hq, down, down_type, N, K, y, M, s);
   }
   // Otherwise: the fused gate/up (with the norm when given), then down.
   status = norm ? qk_ffn_gate_up_norm(x, norm, eps, gate, up, gate_up_type, K, N, h, M, stream)

@@ -128,16 +128,22 @@ def test_ffn_block_other_shapes_one_launch(gpu, oracle, K, N, down_type):
     gpu.ffn_workspace_check(ws)
 
 
-@pytest.mark.parametrize("M,norm", [(2, True), (8, False), (12, True)])
-def test_ffn_block_batched_rows_take_separate_launches(gpu, oracle, M, norm):
+@pytest.mark.parametrize("M,norm,down_type", [(2, True, Q6), (8, False, Q6), (8, True, Q4), (5, True, Q6),
+                                               (12, True, Q6)])
+def test_ffn_block_batched_rows_take_separate_launches(gpu, oracle, M, norm, down_type):
+    """M = 2..8: norm and Q8(h) in the workspace, h quantised once, the down
+    mat-vec on Q8 blocks; bit-identical to gate/up + qk_matmul (the same Q8
+    codes, row partitions and summation order). M > 8: the prefill path."""
     K, N = 2560, 9728
-    blk = Block(gpu, oracle, K, N, Q6, M, norm, SEED + 100 + M)
+    blk = Block(gpu, oracle, K, N, down_type, M, norm, SEED + 100 + M + down_type)
     ws, nbytes = _workspace(gpu)
     h, y, launch = blk.run(ws, nbytes)
-    print(f"[case] ffn M={M} launch {launch}", flush=True)
+    print(f"[case] ffn M={M} down={down_type} norm={norm} launch {launch}", flush=True)
     assert not launch.startswith("ffn_fused_kernel")
     if M <= 8:
         blk.check(oracle, h, y)
+        hs, ys = blk.separate()
+        assert np.array_equal(h, hs) and np.array_equal(y, ys)
     else:  # the prefill GEMM's fp16 split products: within the path's bar
         h_ref = blk.oracle_h(oracle)
         assert oracle.row_norm_error(h, h_ref) <= 1e-5
@@ -145,27 +151,29 @@ def test_ffn_block_batched_rows_take_separate_launches(gpu, oracle, M, norm):
         assert oracle.row_norm_error(y, y_own) <= 1e-5
 
 
-def test_ffn_block_graph_replays(gpu, oracle):
-    """The one-launch block captured in a graph, replayed with eager calls and
-    synchronisations in between: every replay equals the eager result."""
+@pytest.mark.parametrize("M", [1, 8])
+def test_ffn_block_graph_replays(gpu, oracle, M):
+    """The block captured in a graph (M = 1: the one launch; M = 8: norm,
+    gate/up, Q8(h) and down through the workspace), replayed with eager calls
+    and synchronisations in between: every replay equals the eager result."""
     qk = gpu
     K, N = 2560, 9728
-    blk = Block(qk, oracle, K, N, Q6, 1, True, SEED + 300)
+    blk = Block(qk, oracle, K, N, Q6, M, True, SEED + 300 + M)
     ws, nbytes = _workspace(qk)
     stream = qk.Stream()
-    h = qk.DeviceBuffer(4 * N)
-    y = qk.DeviceBuffer(4 * K)
+    h = qk.DeviceBuffer(4 * M * N)
+    y = qk.DeviceBuffer(4 * M * K)
 
     def record():
-        qk.ffn(blk.xd, blk.sd, blk.eps, blk.gate, blk.up, Q4, blk.down, Q6, K, N, h, y, 1, ws, nbytes, stream)
+        qk.ffn(blk.xd, blk.sd, blk.eps, blk.gate, blk.up, Q4, blk.down, Q6, K, N, h, y, M, ws, nbytes, stream)
 
     record()
     stream.synchronize()
     eager = (h.download(np.float32), y.download(np.float32))
     graph = qk.Graph.capture(stream, lambda: [record() for _ in range(3)])
     for rep in range(4):
-        y.upload(np.full(K, np.nan, np.float32))
-        h.upload(np.full(N, np.nan, np.float32))
+        y.upload(np.full(M * K, np.nan, np.float32))
+        h.upload(np.full(M * N, np.nan, np.float32))
         graph.launch(stream)
         stream.synchronize()
         assert np.array_equal(h.download(np.float32), eager[0]), f"replay {rep}"
