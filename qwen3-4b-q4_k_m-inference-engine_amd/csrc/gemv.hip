@@ -98,10 +98,12 @@ int matvec_rows_per_launch(int64_t K) {
 }
 
 hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
-  // M = 2..8 with fp32 activations: the batched mat-vec on the matrix cores
-  // (bmv.hip).
+  // M = 2..8: the whole-share batched mat-vec on the matrix cores
+  // (bmv_ws.hip), else (gate/up) the batched mat-vec (bmv.hip).
   bool launched = false;
-  hipError_t e = launch_bmv(p, mode, stream, launched);
+  hipError_t e = launch_bmv_ws(p, mode, stream, launched);
+  if (e != hipSuccess || launched) return e;
+  e = launch_bmv(p, mode, stream, launched);
   if (e != hipSuccess || launched) return e;
   // Shapes whose per-CU share fits in LDS take the whole-share kernel
   // (gemv_stream.hip).

@@ -70,6 +70,12 @@ hipError_t launch_stream_matvec(const MatvecParams& p, int mode, hipStream_t str
 // set) when it takes the shape.
 hipError_t launch_pass_matvec(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
 
+// The whole-share batched mat-vec on the int8 matrix cores (bmv_ws.hip): M =
+// 2..8 rows of fp32 activations (modes 0 and 1) or of Q8 blocks (mode 0);
+// launched (and `launched` set) when every workgroup's rows fit its phased
+// LDS plan.
+hipError_t launch_bmv_ws(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
+
 // The batched mat-vec on the int8 matrix cores (bmv.hip): M = 2..8 rows of
 // fp32 activations, modes 0 and 1; launched (and `launched` set) when the
 // shape fits its LDS plan.

@@ -464,15 +464,15 @@ def _one_hot_q4k(K):
     return w.reshape(-1)
 
 
-@pytest.mark.parametrize("M", [1, 4, 8])
-def test_prologue_quantisation_bitwise(gpu, oracle, M):
+@pytest.mark.parametrize("M,K", [(1, 9728), (4, 9728), (8, 9728), (8, 2560), (3, 2560)])
+def test_prologue_quantisation_bitwise(gpu, oracle, M, K):
     """The in-launch Q8 quantiser (reciprocal + Markstein correction; M = 1: the
-    whole-share kernel, M = 2..8: the matrix-core kernel) gives the reference's
-    round trip round(x/amax*127) * (amax/127) (src/cuda/matmul.cu:8-22,
+    whole-share kernel, M = 2..8: the matrix-core kernels, K = 2560 the
+    whole-share one) gives the reference's round trip round(x/amax*127) *
+    (amax/127) (src/cuda/matmul.cu:8-22,
     src/tests/reference/MatmulReference.hpp:11-29) exactly at every
     position: with the one-hot weights each output is one code times its block
     scale, and every other term of its sums is an exact zero."""
-    K = 9728
     x = _quantiser_input(K, M)
     w = gpu.DeviceBuffer.from_array(_one_hot_q4k(K))
     got = run_matmul(gpu, w, Q4, K, K, x, M)
@@ -482,6 +482,29 @@ def test_prologue_quantisation_bitwise(gpu, oracle, M):
     # where the integer codes give +0.0; every other value matches exactly
     bad = np.nonzero(got != ref)
     assert bad[0].size == 0, f"{bad[0].size} mismatches, first at (m, k) = ({bad[0][0]}, {bad[1][0]})"
+
+
+@pytest.mark.parametrize("name", ["attn_q", "attn_v", "attn_output", "ffn_gate"])
+@pytest.mark.parametrize("M", [2, 8])
+def test_matmul_q8_batched_qwen3_shapes(gpu, oracle, name, M):
+    """qk_quantize_q8 + qk_matmul_q8 (the caller-quantised input of
+    src/cuda/matmul.cu's two launches) at M = 2 and 8 on the full Qwen3
+    shapes: the oracle's product of the same x, and the fp32-input launch's
+    sums (same codes, another kernel's order)."""
+    qtype, K, N = SHAPES[name]
+    w, w_host = batch_weight(gpu, oracle, name)
+    x = oracle.synth_normal(M * K, SEED + 70 + M)
+    xd = gpu.DeviceBuffer.from_array(x)
+    q8 = gpu.DeviceBuffer(M * K // 32 * gpu.Q8_BLOCK_BYTES)
+    y = gpu.DeviceBuffer(4 * M * N)
+    gpu.quantize_q8(xd, M, K, q8)
+    gpu.matmul_q8(q8, w, qtype, K, N, y, M)
+    gpu.synchronize()
+    print(f"[case] q8 {name} type={qtype} K={K} N={N} M={M} launch {gpu.last_launch()}", flush=True)
+    got = y.download(np.float32).reshape(M, N)
+    assert_parity(oracle, got, oracle.reference_product(x, w_host, qtype, K, N))
+    f32 = run_matmul(gpu, w, qtype, K, N, x, M)
+    assert oracle.row_norm_error(got, f32.astype(np.float64)) <= 1e-6
 
 
 def test_quantize_kernel_matches_oracle_and_prologue(gpu, oracle):
