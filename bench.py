@@ -426,7 +426,11 @@ def main() -> int:
         dominant = max(kernels, key=lambda k: kernels[k]["total_us_per_step"])
         d = kernels[dominant]
         roofline = {"bound": "hbm", "achieved": d["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                    "frac": d["frac"], "traffic": measured_traffic(dominant), "kernel": dominant,
+                    "frac": d["frac"], "traffic": measured_traffic(dominant),
+                    "traffic_source": "profiles/traffic_decode_sweep_m1.json: FETCH_SIZE and WRITE_SIZE "
+                                      "rocprofv3 runs of this script, scaled by a 256 MiB copy (not "
+                                      "re-measured in a plain run)",
+                    "kernel": dominant,
                     "avg_launch_us": d["avg_us"], "avg_bytes_per_launch": d["avg_bytes"]}
         log(f"kernels: {json.dumps(kernels)}")
 
