@@ -286,6 +286,25 @@ def prefill_gemm(qk, stream):
                      "frac_of_fp16_mfma_peak": round(flops / (us * 1e6) / PEAK_FP16_TFLOPS, 4)}
         for b in (w, y, ws):
             b.free()
+    # attn q, k and v through qk_matmul_segments_ws (the engine's one call:
+    # one activation prep, one GEMM launch of both weight types)
+    segs = []
+    for i, (qtype, N) in enumerate(((Q4, 4096), (Q4, 1024), (Q6, 1024))):
+        w = qk.DeviceBuffer(N * qk.row_bytes(qtype, K))
+        qk.synth_superblocks(w, qtype, N, K, 20261210 + i, 0.01 if qtype == Q4 else 0.005, 0.01)
+        segs.append((w, qtype, N, qk.DeviceBuffer(4 * M * N)))
+    need = qk.matmul_segments_workspace_size(M, K, segs)
+    ws = qk.DeviceBuffer(need)
+    qk.synchronize()
+    us = time_launches(qk, stream, [lambda: qk.matmul_segments_ws(x, M, K, segs, ws, need, stream)] * 10)
+    flops = 2 * M * K * (4096 + 1024 + 1024)
+    out["attn_qkv_segments"] = {"shape": f"M={M} K={K} q 4096 + k 1024 Q4_K, v 1024 Q6_K, prep + one GEMM launch",
+                                "avg_us": round(us, 2), "TFLOP/s": round(flops / (us * 1e6), 1),
+                                "frac_of_fp16_mfma_peak": round(flops / (us * 1e6) / PEAK_FP16_TFLOPS, 4)}
+    for w, _, _, y in segs:
+        w.free()
+        y.free()
+    ws.free()
     # the fused FFN entry point at M = 512 (gate and up in one GEMM launch,
     # stream-ordered scratch, SiLU*up), timed eagerly: it allocates per call
     N = 9728

@@ -156,13 +156,16 @@ int run_gemm(const float* x, int64_t M, int64_t K, const qk_segment* segments, i
     if (error != hipSuccess) return hip_fail(error, "matmul workspace allocation failed");
   }
   hipError_t error = qk::launch_gemm_prep(x, M, K, scratch, stream);
-  for (int j = 0; j < count && error == hipSuccess; ++j) {
+  // every matrix in one launch when they share its tile plan (attn q, k and v:
+  // one grid of 768 tiles at M = 512 instead of 640 + 128); otherwise two of
+  // one type together where they can, the rest one launch each
+  bool all = false;
+  if (error == hipSuccess && count > 1)
+    error = qk::launch_gemm_core_multi(scratch, segments, count, K, M, stream, all);
+  for (int j = 0; j < count && error == hipSuccess && !all; ++j) {
     if (j + 1 < count && segments[j + 1].type == segments[j].type) {
-      // two matrices of one type in one launch fill more CUs (attn q and k)
       bool launched = false;
-      error = qk::launch_gemm_core_pair(scratch, segments[j].type, K, M, segments[j].w,
-                                        segments[j].N, segments[j].y, segments[j + 1].w,
-                                        segments[j + 1].N, segments[j + 1].y, stream, launched);
+      error = qk::launch_gemm_core_multi(scratch, segments + j, 2, K, M, stream, launched);
       if (error != hipSuccess) break;
       if (launched) {
         ++j;

@@ -211,14 +211,11 @@ hipError_t launch_gemm_core(const void* workspace, const void* w, int type, int6
   return launch_gemm_kq(type, ws.hi, ws.row_scale, ws.xs, w, K, N, y, M, partials, stream);
 }
 
-hipError_t launch_gemm_core_pair(const void* workspace, int type, int64_t K, int64_t M,
-                                 const void* w0, int64_t N0, float* y0, const void* w1, int64_t N1,
-                                 float* y1, hipStream_t stream, bool& launched) {
+hipError_t launch_gemm_core_multi(const void* workspace, const qk_segment* segments, int count,
+                                  int64_t K, int64_t M, hipStream_t stream, bool& launched) {
   launched = false;
   const WorkspaceLayout ws = layout(const_cast<void*>(workspace), M, K);
-  if (!gemm_kq_fits(M, K, N0) || !gemm_kq_fits(M, K, N1)) return hipErrorInvalidValue;
-  return launch_gemm_kq_pair(type, ws.hi, ws.row_scale, ws.xs, w0, N0, y0, w1, N1, y1, K, M, stream,
-                             launched);
+  return launch_gemm_kq_multi(ws.hi, ws.row_scale, ws.xs, segments, count, K, M, stream, launched);
 }
 
 }  // namespace qk

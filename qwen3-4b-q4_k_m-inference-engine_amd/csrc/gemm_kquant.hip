@@ -74,21 +74,21 @@ struct KQCfg {
   static_assert(PIECES >= 1 && SLOT % (16 * 64 * kWaves) == 0, "whole pieces per thread");
 };
 
+constexpr int kKQMaxSegments = 4;
+
 struct KQGemmArgs {
   const _Float16* hi;  // [M x K]; lo follows at + M*K
   const _Float16* xs;  // sub-block sums: [M][S][hi 8, lo 8] (Q4_K only)
   const float* row_scale;
-  const uint8_t* w;
-  float* y;
-  int32_t M, N, K, S;
-  float* part;  // splits > 1: unscaled partial products [splits][M][N]
+  int32_t M, K, S, nseg;
+  float* part;  // splits > 1 (one matrix): unscaled partial products [splits][M][N]
   int32_t n_tiles, tiles, per_xcd, splits;
-  // A second weight matrix of the same type and K on the same activations
-  // (N1 > 0, one split only): n-tiles from n_tiles0 on are its, written to
-  // y1 [M x N1].
-  const uint8_t* w1;
-  float* y1;
-  int32_t N1, n_tiles0;
+  // The weight matrices of the launch (several share one split-free launch:
+  // attn q, k and v of one activation tile): matrix j covers n-tiles
+  // [tile0[j], tile0[j+1]) and writes y[j] [M x N[j]].
+  const uint8_t* w[kKQMaxSegments];
+  float* y[kKQMaxSegments];
+  int32_t N[kKQMaxSegments], type[kKQMaxSegments], tile0[kKQMaxSegments];
 };
 
 // 8 weights (bytes of dwords lo, hi; nibble U) -> fp16 sc*q.
@@ -135,33 +135,16 @@ __device__ __forceinline__ void weights_q6k(uint32_t l0, uint32_t l1, uint32_t h
   bl = half8{lo[0].x, lo[0].y, lo[1].x, lo[1].y, lo[2].x, lo[2].y, lo[3].x, lo[3].y};
 }
 
+// One output tile (m-tile mt, n-tile nt of matrix wmat [N rows]) of one K
+// split; `slots` is the workgroup's activation staging.
 template <int TYPE, int TM, int TN>
-__global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArgs args) {
+__device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)[2][KQCfg<TM, TN>::SLOT],
+                                        int mt, int nt, int split, const uint8_t* wmat, float* ymat,
+                                        int N) {
   using C = KQCfg<TM, TN>;
   constexpr bool kQ6 = TYPE == QK_TYPE_Q6_K;
   constexpr int B = kQ6 ? kQ6KBytes : kQ4KBytes;  // superblock bytes
   constexpr int QW = kQ6 ? 2 : 1;                 // 16-byte weight loads per stage and n-tile
-  __shared__ __align__(16) uint8_t slots[2][C::SLOT];
-  const int b = static_cast<int>(blockIdx.x);
-  // Consecutive tiles go to one XCD (workgroups are dealt to the 8 XCDs in
-  // turn) and run along N first, so an XCD keeps one activation tile in its
-  // L2 while the weight tiles stream past it.
-  // Work unit u = tile * splits + split: split covers superblocks
-  // [sb0, sb1) of K (splits > 1 when the tiles alone leave CUs idle).
-  const int u = (b & 7) * args.per_xcd + (b >> 3);
-  if ((b >> 3) >= args.per_xcd || u >= args.tiles * args.splits) return;
-  const int t = u / args.splits, split = u % args.splits;
-  const int mt = t / args.n_tiles;
-  int nt = t % args.n_tiles;
-  const uint8_t* wmat = args.w;
-  float* ymat = args.y;
-  int N = args.N;
-  if (args.N1 > 0 && nt >= args.n_tiles0) {  // the second matrix's tiles
-    wmat = args.w1;
-    ymat = args.y1;
-    N = args.N1;
-    nt -= args.n_tiles0;
-  }
   const int m0 = mt * C::BM, n0 = nt * C::BN;
   const int M = args.M, K = args.K, S = args.S;
   const int sb0 = split * S / args.splits, sb1 = (split + 1) * S / args.splits;
@@ -458,6 +441,45 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArg
     }
 }
 
+// TYPE: the weight type of every matrix of the launch, or 0 for matrices of
+// both types (each workgroup takes its matrix's).
+template <int TYPE, int TM, int TN>
+__global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArgs args) {
+  using C = KQCfg<TM, TN>;
+  __shared__ __align__(16) uint8_t slots[2][C::SLOT];
+  const int b = static_cast<int>(blockIdx.x);
+  // Consecutive tiles go to one XCD (workgroups are dealt to the 8 XCDs in
+  // turn) and run along N first, so an XCD keeps one activation tile in its
+  // L2 while the weight tiles stream past it.
+  // Work unit u = tile * splits + split: split covers superblocks
+  // [sb0, sb1) of K (splits > 1 when the tiles alone leave CUs idle).
+  const int u = (b & 7) * args.per_xcd + (b >> 3);
+  if ((b >> 3) >= args.per_xcd || u >= args.tiles * args.splits) return;
+  const int t = u / args.splits, split = u % args.splits;
+  const int mt = t / args.n_tiles;
+  const int nt = t % args.n_tiles;
+  // the n-tile's matrix, field by field (a struct picked by a runtime index
+  // would be copied to scratch memory)
+  const int nseg = args.nseg;
+  const int j = (nseg > 1 && nt >= args.tile0[1]) + (nseg > 2 && nt >= args.tile0[2]) +
+                (nseg > 3 && nt >= args.tile0[3]);
+  auto pick = [j](auto f0, auto f1, auto f2, auto f3) {
+    return j == 0 ? f0 : j == 1 ? f1 : j == 2 ? f2 : f3;
+  };
+  const uint8_t* wmat = pick(args.w[0], args.w[1], args.w[2], args.w[3]);
+  float* ymat = pick(args.y[0], args.y[1], args.y[2], args.y[3]);
+  const int N = pick(args.N[0], args.N[1], args.N[2], args.N[3]);
+  const int nt_local = nt - pick(args.tile0[0], args.tile0[1], args.tile0[2], args.tile0[3]);
+  if constexpr (TYPE != 0) {
+    kq_tile<TYPE, TM, TN>(args, slots, mt, nt_local, split, wmat, ymat, N);
+  } else {
+    if (pick(args.type[0], args.type[1], args.type[2], args.type[3]) == QK_TYPE_Q4_K)
+      kq_tile<QK_TYPE_Q4_K, TM, TN>(args, slots, mt, nt_local, split, wmat, ymat, N);
+    else
+      kq_tile<QK_TYPE_Q6_K, TM, TN>(args, slots, mt, nt_local, split, wmat, ymat, N);
+  }
+}
+
 // y[m][n] = (partial 0 + partial 1 + ...) * 2^-s(m), the splits added in
 // order (results do not depend on timing). Grid (ceil(N / 256), M).
 __global__ __launch_bounds__(256) void gemm_kq_reduce_kernel(const float* __restrict__ part,
@@ -476,8 +498,11 @@ __global__ __launch_bounds__(256) void gemm_kq_reduce_kernel(const float* __rest
 template <int TYPE, int TM, int TN>
 hipError_t launch_cfg(KQGemmArgs a, hipStream_t stream) {
   using C = KQCfg<TM, TN>;
-  a.n_tiles0 = (a.N + C::BN - 1) / C::BN;
-  a.n_tiles = a.n_tiles0 + (a.N1 > 0 ? (a.N1 + C::BN - 1) / C::BN : 0);
+  a.n_tiles = 0;
+  for (int j = 0; j < a.nseg; ++j) {
+    a.tile0[j] = a.n_tiles;
+    a.n_tiles += (a.N[j] + C::BN - 1) / C::BN;
+  }
   a.tiles = a.n_tiles * ((a.M + C::BM - 1) / C::BM);
   a.per_xcd = (a.tiles * a.splits + 7) / 8;
   note("gemm_kq_kernel", 8 * a.per_xcd, TYPE, TM, TN, a.splits);
@@ -536,11 +561,13 @@ hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, 
   a.hi = hi;
   a.xs = static_cast<const _Float16*>(xsums);
   a.row_scale = row_scale;
-  a.w = static_cast<const uint8_t*>(w);
-  a.y = y;
+  a.nseg = 1;
+  a.w[0] = static_cast<const uint8_t*>(w);
+  a.y[0] = y;
+  a.N[0] = static_cast<int32_t>(N);
+  a.type[0] = type;
   a.part = partials;
   a.M = static_cast<int32_t>(M);
-  a.N = static_cast<int32_t>(N);
   a.K = static_cast<int32_t>(K);
   a.S = static_cast<int32_t>(K / 256);
   a.splits = p.splits;
@@ -557,30 +584,53 @@ hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, 
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_kq_pair(int type, const _Float16* hi, const float* row_scale,
-                               const void* xsums, const void* w0, int64_t N0, float* y0,
-                               const void* w1, int64_t N1, float* y1, int64_t K, int64_t M,
-                               hipStream_t stream, bool& launched) {
+hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, const void* xsums,
+                                const qk_segment* segments, int count, int64_t K, int64_t M,
+                                hipStream_t stream, bool& launched) {
   launched = false;
-  // planned as one matrix of N0 + N1 columns; a split K stays per matrix
-  const KQPlan p = plan(type, M, N0 + N1, K);
-  if (p.splits > 1 || !gemm_kq_fits(M, K, N0 + N1)) return hipSuccess;
+  if (count < 2 || count > kKQMaxSegments) return hipSuccess;
+  // One launch when every matrix would run unsplit on the tile shape the
+  // combined grid takes: each tile then does exactly the work of its own
+  // launch (outputs bit for bit the same), in one grid that fills the CUs.
+  // Q6_K matrices first: their tiles take longer, so they start first.
+  int order[kKQMaxSegments], n = 0;
+  bool q4 = false, q6 = false;
+  int64_t total = 0;
+  for (int pass = 0; pass < 2; ++pass)
+    for (int j = 0; j < count; ++j)
+      if ((segments[j].type == QK_TYPE_Q6_K) == (pass == 0)) order[n++] = j;
+  for (int j = 0; j < count; ++j) {
+    if (!gemm_kq_fits(M, K, segments[j].N) || plan(segments[j].type, M, segments[j].N, K).splits > 1)
+      return hipSuccess;
+    (segments[j].type == QK_TYPE_Q4_K ? q4 : q6) = true;
+    total += segments[j].N;
+  }
+  if (!gemm_kq_fits(M, K, total)) return hipSuccess;
+  const int type = q4 && q6 ? 0 : q4 ? QK_TYPE_Q4_K : QK_TYPE_Q6_K;
+  const KQPlan p = plan(type == 0 ? QK_TYPE_Q4_K : type, M, total, K);
+  for (int j = 0; j < count; ++j)
+    if (plan(segments[j].type, M, segments[j].N, K).wide != p.wide) return hipSuccess;
+  if (type == 0 && p.wide) return hipSuccess;  // the mixed kernel is instantiated for 32 x 128 tiles
   KQGemmArgs a{};
   a.hi = hi;
   a.xs = static_cast<const _Float16*>(xsums);
   a.row_scale = row_scale;
-  a.w = static_cast<const uint8_t*>(w0);
-  a.y = y0;
-  a.w1 = static_cast<const uint8_t*>(w1);
-  a.y1 = y1;
+  a.nseg = count;
+  for (int i = 0; i < count; ++i) {
+    const qk_segment& sg = segments[order[i]];
+    a.w[i] = static_cast<const uint8_t*>(sg.w);
+    a.y[i] = sg.y;
+    a.N[i] = static_cast<int32_t>(sg.N);
+    a.type[i] = sg.type;
+  }
   a.M = static_cast<int32_t>(M);
-  a.N = static_cast<int32_t>(N0);
-  a.N1 = static_cast<int32_t>(N1);
   a.K = static_cast<int32_t>(K);
   a.S = static_cast<int32_t>(K / 256);
   a.splits = 1;
   hipError_t e;
-  if (type == QK_TYPE_Q6_K)
+  if (type == 0)
+    e = launch_cfg<0, 1, 1>(a, stream);
+  else if (type == QK_TYPE_Q6_K)
     e = p.wide ? launch_cfg<QK_TYPE_Q6_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q6_K, 1, 1>(a, stream);
   else
     e = p.wide ? launch_cfg<QK_TYPE_Q4_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q4_K, 1, 1>(a, stream);

@@ -140,16 +140,16 @@ hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, 
                           const void* w, int64_t K, int64_t N, float* y, int64_t M, float* partials,
                           hipStream_t stream);
 
-// Two weight matrices of one type and width K on the same prepared
-// activations in one launch (q and k of attention): launched (and `launched`
-// set) when neither needs a split K, else nothing is enqueued.
-hipError_t launch_gemm_kq_pair(int type, const _Float16* hi, const float* row_scale,
-                               const void* xsums, const void* w0, int64_t N0, float* y0,
-                               const void* w1, int64_t N1, float* y1, int64_t K, int64_t M,
-                               hipStream_t stream, bool& launched);
-hipError_t launch_gemm_core_pair(const void* workspace, int type, int64_t K, int64_t M,
-                                 const void* w0, int64_t N0, float* y0, const void* w1, int64_t N1,
-                                 float* y1, hipStream_t stream, bool& launched);
+// 2..4 weight matrices of width K (either type) on the same prepared
+// activations in one launch (attn q, k and v; gate and up): launched (and
+// `launched` set) when none needs a split K and all take the combined grid's
+// tile shape, else nothing is enqueued. Each output equals its single launch's
+// bit for bit.
+hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, const void* xsums,
+                                const qk_segment* segments, int count, int64_t K, int64_t M,
+                                hipStream_t stream, bool& launched);
+hipError_t launch_gemm_core_multi(const void* workspace, const qk_segment* segments, int count,
+                                  int64_t K, int64_t M, hipStream_t stream, bool& launched);
 
 // Bytes of the argmax workspace (zero-filled once by the caller).
 size_t argmax_workspace_bytes();

@@ -188,20 +188,23 @@ def test_prefill_entry_points_agree_bitwise(gpu, oracle, qtype):
         gpu.matmul_ws(xd, w, qtype, K, N, yb, M, ws, need - 256)
 
 
-@pytest.mark.parametrize("M,shapes", [
-    (512, [(Q4, 4096), (Q4, 1024), (Q6, 1024)]),   # attn q, k (one launch) and v
-    (77, [(Q6, 333), (Q6, 129), (Q4, 200), (Q4, 64)]),
+@pytest.mark.parametrize("M,K,shapes", [
+    (512, 2560, [(Q4, 4096), (Q4, 1024), (Q6, 1024)]),   # attn q, k and v: one launch of both types
+    (77, 2560, [(Q6, 333), (Q6, 129), (Q4, 200), (Q4, 64)]),
+    (40, 2560, [(Q4, 4096), (Q4, 1024), (Q6, 1024)]),
+    (64, 9728, [(Q6, 256), (Q4, 300)]),                    # split K: separate launches
 ])
-def test_prefill_segments_pairs_match_single_launches(gpu, oracle, M, shapes):
-    """qk_matmul_segments at M > 8 runs two same-type matrices in one GEMM
-    launch: every output equals its single-matrix qk_matmul bit for bit, and
-    the oracle within the bar."""
-    K = 2560
+def test_prefill_segments_pairs_match_single_launches(gpu, oracle, M, K, shapes):
+    """qk_matmul_segments at M > 8 runs its matrices in one GEMM launch when
+    none needs a split K (each workgroup takes its matrix's type), otherwise
+    same-type pairs or single launches: every output equals its
+    single-matrix qk_matmul bit for bit, and the oracle within the bar."""
     ws = [make_weight(gpu, q, N, K, SEED + 60 + i) for i, (q, N) in enumerate(shapes)]
     x = oracle.synth_normal(M * K, SEED + 61)
     xd = gpu.DeviceBuffer.from_array(x)
     ys = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes]
     gpu.matmul_segments(xd, M, K, [(w, q, N, y) for w, (q, N), y in zip(ws, shapes, ys)])
+    print(f"[case] segments M={M} K={K} {shapes} last launch {gpu.last_launch()}", flush=True)
     singles = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes]
     for w, (q, N), y in zip(ws, shapes, singles):
         gpu.matmul(xd, w, q, K, N, y, M)
