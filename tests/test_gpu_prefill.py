@@ -255,7 +255,8 @@ def test_prefill_graph_replay_with_workspace(gpu, oracle):
 def test_ffn_gate_up_workspace_variant_and_deep_k(gpu, oracle, qtype, K, N, M):
     """qk_ffn_gate_up_ws equals qk_ffn_gate_up bit for bit; the deep-K shape
     (K = 9728, N = 2560) takes the split-K GEMM for gate and up in separate
-    launches, checked against the oracle."""
+    launches, checked against the oracle; a workspace short of
+    qk_ffn_gate_up_workspace_size is rejected."""
     gate = make_weight(gpu, qtype, N, K, SEED + 60)
     up = make_weight(gpu, qtype, N, K, SEED + 61)
     x = oracle.synth_normal(M * K, SEED + 62)
@@ -297,3 +298,32 @@ def test_segments_workspace_variant(gpu, oracle):
     gpu.synchronize()
     for a, b in zip(y1, y2):
         assert np.array_equal(a.download(np.float32), b.download(np.float32))
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 2560, 9728), (77, 2560, 1000), (40, 512, 300), (33, 9728, 2560)])
+def test_ffn_gate_up_matches_separate_kernels(gpu, oracle, M, K, N):
+    """qk_ffn_gate_up at M > 8 (gate and up in one GEMM launch unless K splits,
+    then the SiLU kernel): h equals qk_matmul(gate), qk_matmul(up) and
+    qk_silu_multiply bit for bit, and the oracle's SiLU(x . gate^T) *
+    (x . up^T) within the bar."""
+    gate = make_weight(gpu, Q4, N, K, SEED + 70)
+    up = make_weight(gpu, Q4, N, K, SEED + 71)
+    x = oracle.synth_normal(M * K, SEED + 72)
+    xd = gpu.DeviceBuffer.from_array(x)
+    h = gpu.DeviceBuffer.from_array(np.full(M * N, np.nan, np.float32))
+    gpu.ffn_gate_up(xd, gate, up, Q4, K, N, h, M)
+    gpu.synchronize()
+    print(f"[case] ffn gate/up M={M} K={K} N={N} launch {gpu.last_launch()}", flush=True)
+    yg, yu, hs = (gpu.DeviceBuffer(4 * M * N) for _ in range(3))
+    gpu.matmul(xd, gate, Q4, K, N, yg, M)
+    gpu.matmul(xd, up, Q4, K, N, yu, M)
+    gpu.silu_multiply(yg, yu, hs, M * N)
+    gpu.synchronize()
+    got = h.download(np.float32)
+    assert np.array_equal(got, hs.download(np.float32))
+    if N <= 1000:
+        g = float64_reference(oracle, x, gate.download(np.uint8), Q4, K, N, M)
+        u = float64_reference(oracle, x, up.download(np.uint8), Q4, K, N, M)
+        with np.errstate(over="ignore"):
+            ref = g / (1.0 + np.exp(-g)) * u
+        check(oracle, got.reshape(M, N), ref, f"ffn gate/up M={M}")
