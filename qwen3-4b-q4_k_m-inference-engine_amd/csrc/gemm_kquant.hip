@@ -227,15 +227,17 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
     for (int i = 0; i < TM; ++i) x[i] = load16(xrow[i] + 16 * sb);
   };
 
-  // acc: the output tile; ph / pl: this superblock's hi and lo products
-  // (separate accumulators: independent MFMA chains)
-  f32x16 acc[TM][TN], ph[TM][TN], pl[TM][TN];
+  // acc: the output tile; ph: this superblock's products, both activation
+  // planes (and for Q6_K the weight remainder) accumulated into one chain per
+  // tile (a second accumulator per tile cost 32 VGPRs at TM = 2, the margin
+  // between two and three workgroups per CU)
+  f32x16 acc[TM][TN], ph[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = ph[i][j][r] = pl[i][j][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = ph[i][j][r] = 0.0f;
 
   // In flight across stages: areg (activations, loaded in stage c-1 and
   // stored to LDS in stage c for stage c+1), bq[p] (qs bytes of the stages of
@@ -297,9 +299,11 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
       }
 
       // Steps: the MFMAs of step s interleaved with the weight conversion of
-      // step s+1 and the A fragment reads of step s+2 (two fragment buffers);
-      // the stage's activation staging (store of stage c+1, loads of stage
-      // c+3) sits between steps 1 and 2, under their MFMAs.
+      // step s+1 and the A fragment reads of step s+kAB (kAB fragment
+      // buffers: two for one m-tile; one at TM = 2, where the second buffer's
+      // 16 VGPRs would hold the kernel to two workgroups per CU); the stage's
+      // activation staging (store of stage c+1, loads of stage c+3) sits
+      // between steps 1 and 2, under their MFMAs.
       const lds_byte* a_row = (const lds_byte*)slots[g & 1] + l32 * 256;
       auto read_a = [&](int step, half8 (&ah)[TM], half8 (&al)[TM]) {
         const int p = 4 * (step >> 1) + 2 * h + (step & 1);
@@ -327,9 +331,10 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
           }
         }
       };
-      half8 ah[2][TM], al[2][TM], bw[2][TN], bx[2][TN];
+      constexpr int kAB = TM >= 2 ? 1 : 2;
+      half8 ah[kAB][TM], al[kAB][TM], bw[2][TN], bx[2][TN];
       read_a(0, ah[0], al[0]);
-      read_a(1, ah[1], al[1]);
+      if constexpr (kAB == 2) read_a(1, ah[1], al[1]);
       convert(0, bw[0], bx[0]);
 #pragma unroll
       for (int step = 0; step < 4; ++step) {
@@ -337,13 +342,14 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
-            ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[step & 1][i], bw[step & 1][j], ph[i][j], 0, 0, 0);
-            pl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[step & 1][i], bw[step & 1][j], pl[i][j], 0, 0, 0);
+            const int ab = step % kAB;
+            ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[ab][i], bw[step & 1][j], ph[i][j], 0, 0, 0);
+            ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[ab][i], bw[step & 1][j], ph[i][j], 0, 0, 0);
             if constexpr (kQ6)
-              ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[step & 1][i], bx[step & 1][j], ph[i][j], 0, 0, 0);
+              ph[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[ab][i], bx[step & 1][j], ph[i][j], 0, 0, 0);
           }
         if (step < 3) convert(step + 1, bw[(step + 1) & 1], bx[(step + 1) & 1]);
-        if (step < 2) read_a(step + 2, ah[step & 1], al[step & 1]);
+        if (step + kAB < 4) read_a(step + kAB, ah[step % kAB], al[step % kAB]);
         if (step == 1) {
           // stage c+1's activations (loaded a stage ago) into the other
           // slot, then start loading stage c+2 into the same registers
@@ -374,9 +380,8 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
             const float d = half_bits_to_float(dcur[j]);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              acc[i][j][r] = fmaf(d, ph[i][j][r] + pl[i][j][r], acc[i][j][r]);
+              acc[i][j][r] = fmaf(d, ph[i][j][r], acc[i][j][r]);
               ph[i][j][r] = 0.0f;
-              pl[i][j][r] = 0.0f;
             }
           }
       }
@@ -392,7 +397,7 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(dd[j], ph[i][j][r] + pl[i][j][r], acc[i][j][r]);
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(dd[j], ph[i][j][r], acc[i][j][r]);
             f32x16 zero;
 #pragma unroll
             for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
@@ -407,7 +412,6 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
             for (int r = 0; r < 16; ++r) {
               acc[i][j][r] = fmaf(dm[j], ph[i][j][r], acc[i][j][r]);
               ph[i][j][r] = 0.0f;
-              pl[i][j][r] = 0.0f;
             }
         load_x(min(sb + 1, sb1 - 1), xa);
       }
@@ -442,9 +446,13 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
 }
 
 // TYPE: the weight type of every matrix of the launch, or 0 for matrices of
-// both types (each workgroup takes its matrix's).
+// both types (each workgroup takes its matrix's). Register budget: three
+// workgroups per CU (168 VGPRs) except the Q6_K kernels, whose 64-row tile
+// needs more (two per CU). At TM = 2 the Q4_K kernel fits 168 with 7 dwords
+// spilled (pointers reloaded once per superblock pair): ffn_gate at M = 512,
+// 608 tiles, then runs as one round instead of 512 tiles plus a 96-tile round.
 template <int TYPE, int TM, int TN>
-__global__ __launch_bounds__(64 * kWaves, 2) void gemm_kq_kernel(const KQGemmArgs args) {
+__global__ __launch_bounds__(64 * kWaves, TYPE == QK_TYPE_Q6_K ? 2 : 3) void gemm_kq_kernel(const KQGemmArgs args) {
   using C = KQCfg<TM, TN>;
   __shared__ __align__(16) uint8_t slots[2][C::SLOT];
   const int b = static_cast<int>(blockIdx.x);
