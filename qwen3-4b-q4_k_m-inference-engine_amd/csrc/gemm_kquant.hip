@@ -178,10 +178,15 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
   for (int j = 0; j < TN; ++j)
     wrow[j] = wmat +
               static_cast<int64_t>(min(n0 + wave * 32 * TN + 32 * j + l32, N - 1)) * S * B;
-  const _Float16* xrow[TM];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-    xrow[i] = args.xs + static_cast<int64_t>(min(m0 + 32 * i + l32, M - 1)) * S * 16 + 8 * h;
+  // The sub-block sum row of m-tile i is formed where it is used: a pointer
+  // held across the superblock loop is a register the 64-row tile cannot
+  // spare (the compiler hoisted it out of the loop and spilled it there; the
+  // lane index read through asm keeps the computation at its use).
+  auto xrow = [&](int i) {
+    int t;
+    asm volatile("v_and_b32 %0, 63, %1" : "=v"(t) : "v"(static_cast<int>(threadIdx.x)));
+    return args.xs + static_cast<int64_t>(min(m0 + 32 * i + (t & 31), M - 1)) * S * 16 + 8 * (t >> 5);
+  };
 
   auto load_a = [&](int c, u32x4 (&r)[C::PIECES]) {
 #pragma unroll
@@ -224,7 +229,7 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
   };
   auto load_x = [&](int sb, u32x4 (&x)[TM]) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) x[i] = load16(xrow[i] + 16 * sb);
+    for (int i = 0; i < TM; ++i) x[i] = load16(xrow(i) + 16 * sb);
   };
 
   // acc: the output tile; ph: this superblock's products, both activation
@@ -243,7 +248,7 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
   // stored to LDS in stage c for stage c+1), bq[p] (qs bytes of the stages of
   // parity p, loaded a stage ahead), wh[p] (headers of the superblocks of
   // parity p, loaded during the superblock before) and xa (this superblock's
-  // sub-block sums). Every loaded dword is used, so no load destination is
+  // sub-block sums, loaded in its stage 2). Every loaded dword is used, so no load destination is
   // recycled early, and the superblock loop is unrolled by two so no loaded
   // register is copied at the loop edge.
   u32x4 areg[C::PIECES], wh[2][TN], bq[2][TN][QW], xa[TM];
@@ -251,7 +256,6 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
   load_a(4 * sb0, areg);
   load_head(sb0, wh[0], wd[0]);
   load_q(4 * sb0, bq[0]);
-  if constexpr (!kQ6) load_x(sb0, xa);
   store_a(0, areg);
   load_a(min(4 * sb0 + 1, c_last), areg);
   __syncthreads();
@@ -259,7 +263,6 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
   const int swz = l32 & 15;  // row & 15 of every A row this lane reads
   auto superblock = [&](int sb, const u32x4 (&hcur)[TN], const uint32_t (&dcur)[TN],
                         u32x4 (&hnext)[TN], uint32_t (&dnext)[TN]) {
-    u32x4 min_b[TN];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int c = 4 * sb + g;
@@ -293,9 +296,8 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
         const half2v t1{s1, s1};
         cm[j][1] = t1 * half2v{0.0625f16, 0.0625f16};
         ce[j][1] = t1 * half2v{-64.0f16, -64.0f16};
-        const half2v mm{static_cast<_Float16>(static_cast<uint16_t>(mn0)),
-                        static_cast<_Float16>(static_cast<uint16_t>(mn1))};
-        min_b[j][g] = __builtin_bit_cast(uint32_t, mm);
+        (void)mn0;  // the mins enter at the superblock's end
+        (void)mn1;
       }
 
       // Steps: the MFMAs of step s interleaved with the weight conversion of
@@ -359,6 +361,7 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
           // activation loads (vector loads complete in order: the next
           // stage's wait for activations does not wait for these)
           if (g == 2) load_head(min(sb + 1, sb1 - 1), hnext, dnext);
+          if (!kQ6 && g == 2) load_x(sb, xa);
         }
         // one MFMA, then a share of the VALU and LDS work, repeated
 #pragma unroll
@@ -387,10 +390,20 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
       }
       if (!kQ6 && g == 3) {  // superblock end: acc += d * part - 32 dmin * (X . m)
         float dd[TN], dm[TN];
+        u32x4 min_b[TN];  // m_j of the 8 sub-blocks as fp16 (formed here: short-lived)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           dd[j] = half_bits_to_float(hcur[j].x & 0xFFFFu);
           dm[j] = -32.0f * half_bits_to_float(hcur[j].x >> 16);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            int sa, ma, sb2, mb;
+            scale_min_k4(2 * q, hcur[j].y, hcur[j].z, hcur[j].w, sa, ma);
+            scale_min_k4(2 * q + 1, hcur[j].y, hcur[j].z, hcur[j].w, sb2, mb);
+            const half2v mm{static_cast<_Float16>(static_cast<uint16_t>(ma)),
+                            static_cast<_Float16>(static_cast<uint16_t>(mb))};
+            min_b[j][q] = __builtin_bit_cast(uint32_t, mm);
+          }
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -413,7 +426,6 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
               acc[i][j][r] = fmaf(dm[j], ph[i][j][r], acc[i][j][r]);
               ph[i][j][r] = 0.0f;
             }
-        load_x(min(sb + 1, sb1 - 1), xa);
       }
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
@@ -448,9 +460,10 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
 // TYPE: the weight type of every matrix of the launch, or 0 for matrices of
 // both types (each workgroup takes its matrix's). Register budget: three
 // workgroups per CU (168 VGPRs) except the Q6_K kernels, whose 64-row tile
-// needs more (two per CU). At TM = 2 the Q4_K kernel fits 168 with 7 dwords
-// spilled (pointers reloaded once per superblock pair): ffn_gate at M = 512,
-// 608 tiles, then runs as one round instead of 512 tiles plus a 96-tile round.
+// needs more (two per CU). At TM = 2 the Q4_K kernel fits 168 with 3 dwords
+// spilled (epilogue values, stored before the superblock loop and reloaded
+// after it): ffn_gate at M = 512, 608 tiles, then runs as one round instead
+// of 512 tiles plus a 96-tile round.
 template <int TYPE, int TM, int TN>
 __global__ __launch_bounds__(64 * kWaves, TYPE == QK_TYPE_Q6_K ? 2 : 3) void gemm_kq_kernel(const KQGemmArgs args) {
   using C = KQCfg<TM, TN>;
