@@ -539,10 +539,12 @@ struct KQPlan {
 
 // Tile and split choice, planned for MI355X's 256 CUs (correct on any
 // device): 64 x 128 tiles when the grid is large enough, else 32 x 128
-// (twice the workgroups, each half the rows); measured at M = 512: Q4_K takes
-// 64 x 128 from two tiles per CU (ffn_gate) and 32 x 128 below (attn_q/k,
-// attn_output); Q6_K, whose stages cost more, takes 64 x 128 from half a tile
-// per CU (ffn_down) and 32 x 128 below (attn_v). Grids of fewer than two
+// (twice the workgroups, each half the rows). Q4_K takes 64 x 128 from 1.5
+// tiles per CU (measured, N = 9728: M = 384, 456 tiles, 65.7 us against 75.7
+// with 912 narrow tiles; M = 320, 380 tiles, no difference) and 32 x 128
+// below (attn_q/k, attn_output at M = 512); Q6_K, whose stages cost more,
+// takes 64 x 128 from half a tile per CU (ffn_down) and 32 x 128 below
+// (attn_v). The tile height does not change any output element's sums. Grids of fewer than two
 // tiles per CU split a deep K (at most 4 ways, at least 8 superblocks a
 // split) so that about two work units reach every CU; a reduce kernel adds
 // the splits. Measured at M = 512: ffn_down (K = 9728, 3 splits) 102 us
@@ -552,7 +554,7 @@ constexpr int64_t kPlanCUs = 256;
 KQPlan plan(int type, int64_t M, int64_t N, int64_t K) {
   const int64_t tiles64 = ((M + 63) / 64) * ((N + 127) / 128);
   const int64_t tiles32 = ((M + 31) / 32) * ((N + 127) / 128);
-  const bool wide = type == QK_TYPE_Q6_K ? 2 * tiles64 >= kPlanCUs : tiles64 >= 2 * kPlanCUs;
+  const bool wide = type == QK_TYPE_Q6_K ? 2 * tiles64 >= kPlanCUs : 2 * tiles64 >= 3 * kPlanCUs;
   const int64_t tiles = wide ? tiles64 : tiles32;
   const int64_t by_grid = std::clamp<int64_t>(2 * kPlanCUs / tiles, 1, 4);
   const int64_t by_depth = std::max<int64_t>(K / 256 / 8, 1);
@@ -610,10 +612,11 @@ hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, cons
                                 hipStream_t stream, bool& launched) {
   launched = false;
   if (count < 2 || count > kKQMaxSegments) return hipSuccess;
-  // One launch when every matrix would run unsplit on the tile shape the
-  // combined grid takes: each tile then does exactly the work of its own
-  // launch (outputs bit for bit the same), in one grid that fills the CUs.
-  // Q6_K matrices first: their tiles take longer, so they start first.
+  // One launch when every matrix would run unsplit in its own launch: each
+  // tile then does exactly the work of its own launch (outputs bit for bit
+  // the same: the tile height changes no output element's sums), in one grid
+  // that fills the CUs. Q6_K matrices first: their tiles take longer, so they
+  // start first.
   int order[kKQMaxSegments], n = 0;
   bool q4 = false, q6 = false;
   int64_t total = 0;
@@ -628,10 +631,15 @@ hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, cons
   }
   if (!gemm_kq_fits(M, K, total)) return hipSuccess;
   const int type = q4 && q6 ? 0 : q4 ? QK_TYPE_Q4_K : QK_TYPE_Q6_K;
-  const KQPlan p = plan(type == 0 ? QK_TYPE_Q4_K : type, M, total, K);
-  for (int j = 0; j < count; ++j)
-    if (plan(segments[j].type, M, segments[j].N, K).wide != p.wide) return hipSuccess;
-  if (type == 0 && p.wide) return hipSuccess;  // the mixed kernel is instantiated for 32 x 128 tiles
+  // The tile shape of the combined grid. The mixed-type kernel exists for
+  // 32 x 128 tiles only: it is taken while the grid has fewer than two
+  // 64 x 128 tiles per CU (q + k + v at M = 512: 384), else same-type pairs run.
+  bool wide = false;
+  if (type == 0) {
+    if (((M + 63) / 64) * ((total + 127) / 128) >= 2 * kPlanCUs) return hipSuccess;
+  } else {
+    wide = plan(type, M, total, K).wide;
+  }
   KQGemmArgs a{};
   a.hi = hi;
   a.xs = static_cast<const _Float16*>(xsums);
@@ -652,9 +660,9 @@ hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, cons
   if (type == 0)
     e = launch_cfg<0, 1, 1>(a, stream);
   else if (type == QK_TYPE_Q6_K)
-    e = p.wide ? launch_cfg<QK_TYPE_Q6_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q6_K, 1, 1>(a, stream);
+    e = wide ? launch_cfg<QK_TYPE_Q6_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q6_K, 1, 1>(a, stream);
   else
-    e = p.wide ? launch_cfg<QK_TYPE_Q4_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q4_K, 1, 1>(a, stream);
+    e = wide ? launch_cfg<QK_TYPE_Q4_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q4_K, 1, 1>(a, stream);
   launched = e == hipSuccess;
   return e;
 }

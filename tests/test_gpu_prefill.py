@@ -165,6 +165,33 @@ def test_prefill_zero_input_and_reuse(gpu, oracle, qtype):
     s2.destroy()
 
 
+@pytest.mark.parametrize("qtype,N,M_wide,M_narrow", [
+    (Q4, 9728, 384, 320),   # 456 tiles of 64 x 128 against 760 of 32 x 128
+    (Q4, 9728, 512, 256),
+    (Q6, 2560, 512, 96),    # ffn_down-like, K = 2560: 64 x 128 against 32 x 128
+])
+def test_prefill_rows_independent_of_tile_height(gpu, oracle, qtype, N, M_wide, M_narrow):
+    """The launcher picks 64- or 32-row tiles from the grid size; an output
+    row's sums do not depend on it (nor on M): the first M_narrow rows of a
+    launch on 64-row tiles equal a launch of those rows alone on 32-row tiles
+    bit for bit."""
+    K = 2560
+    w = make_weight(gpu, qtype, N, K, SEED + 45)
+    x = oracle.synth_normal(M_wide * K, SEED + 46)
+    xw, xn = gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer.from_array(x[:M_narrow * K])
+    yw, yn = gpu.DeviceBuffer(4 * M_wide * N), gpu.DeviceBuffer(4 * M_narrow * N)
+    gpu.matmul(xw, w, qtype, K, N, yw, M_wide)
+    gpu.synchronize()
+    wide = gpu.last_launch()
+    gpu.matmul(xn, w, qtype, K, N, yn, M_narrow)
+    gpu.synchronize()
+    narrow = gpu.last_launch()
+    print(f"[case] tile height type={qtype} N={N}: M={M_wide} {wide} | M={M_narrow} {narrow}", flush=True)
+    assert wide != narrow  # the two launches took different tile shapes
+    got = yw.download(np.float32)[:M_narrow * N]
+    assert np.array_equal(got, yn.download(np.float32))
+
+
 @pytest.mark.parametrize("qtype", [Q4, Q6])
 def test_prefill_entry_points_agree_bitwise(gpu, oracle, qtype):
     """qk_matmul (stream-ordered scratch) and qk_matmul_ws (caller workspace)
