@@ -518,7 +518,7 @@ int qk_ffn(const float* x, const float* norm, float eps, const void* gate, const
 int qk_ffn_workspace_check(void* workspace, qk_stream_t stream) {
   if (!workspace) return fail(QK_ERR_INVALID_ARGUMENT, "ffn workspace must be non-null");
   uint32_t flag = 0;
-  const size_t at = 256;  // the timeout word's line
+  const size_t at = qk::ffn_timeout_offset();
   hipError_t error = hipMemcpyAsync(&flag, static_cast<char*>(workspace) + at, sizeof(flag),
                                     hipMemcpyDeviceToHost, as_stream(stream));
   if (error == hipSuccess) error = hipStreamSynchronize(as_stream(stream));

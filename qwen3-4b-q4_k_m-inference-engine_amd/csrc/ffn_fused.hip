@@ -36,6 +36,7 @@ int share_depth(int64_t sb, int bytes) {
 }  // namespace
 
 size_t ffn_sync_bytes() { return kFfnSyncBytes; }
+size_t ffn_timeout_offset() { return kSyncTimeout * sizeof(uint32_t); }
 
 hipError_t launch_ffn_fused(const FfnArgs& a, hipStream_t stream, bool& launched) {
   launched = false;

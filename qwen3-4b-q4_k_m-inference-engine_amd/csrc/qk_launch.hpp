@@ -108,6 +108,8 @@ struct FfnArgs {
 hipError_t launch_ffn_fused(const FfnArgs& a, hipStream_t stream, bool& launched);
 // Bytes of the barrier workspace of launch_ffn_fused.
 size_t ffn_sync_bytes();
+// Byte offset in the FFN workspace of the word a timed-out grid barrier sets.
+size_t ffn_timeout_offset();
 
 // Activation rows one launch_matvec can take for width K (its Q8 blocks live
 // in LDS): 8, 4, 2 or 1, or 0 when even one row does not fit.

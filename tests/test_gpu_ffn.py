@@ -115,6 +115,28 @@ def test_ffn_block_qwen3_shape_one_launch(gpu, oracle, down_type, norm):
     gpu.ffn_workspace_check(ws)
 
 
+def test_ffn_workspace_check_reports_and_clears_a_timeout(gpu, oracle):
+    """The grid barrier's bounded wait, when it gives up, sets a word in the
+    workspace (byte 256: the second 256-byte line) and lets the launch end;
+    qk_ffn_workspace_check reports it as QK_ERR_RUNTIME once and clears it.
+    The word is planted from the host here (no kernel is made to time out),
+    then a real launch on the same workspace runs clean and matches."""
+    ws, nbytes = _workspace(gpu)
+    gpu.ffn_workspace_check(ws)  # a zeroed workspace: nothing to report
+    ws.upload(np.array([1], np.uint32), offset=256)
+    with pytest.raises(gpu.QKError, match="grid barrier timed out"):
+        gpu.ffn_workspace_check(ws)
+    assert int(ws.download(np.uint32, 1, offset=256)[0]) == 0
+    gpu.ffn_workspace_check(ws)  # cleared by the report
+    blk = Block(gpu, oracle, 512, 1024, Q6, 1, True, SEED + 7)
+    h, y, launch = blk.run(ws, nbytes)
+    print(f"[case] ffn after a planted timeout word: launch {launch}", flush=True)
+    assert launch.startswith("ffn_fused_kernel")
+    hs, ys = blk.separate()
+    assert np.array_equal(h, hs) and np.array_equal(y, ys)
+    gpu.ffn_workspace_check(ws)
+
+
 @pytest.mark.parametrize("K,N,down_type", [(1024, 3072, Q6), (2048, 6144, Q4), (512, 1024, Q6)])
 def test_ffn_block_other_shapes_one_launch(gpu, oracle, K, N, down_type):
     blk = Block(gpu, oracle, K, N, down_type, 1, True, SEED + K + N)
