@@ -95,7 +95,8 @@ void silu_multiply(const float* gate, const float* up, float* output, size_t cou
 // Index of the largest logit: lowest index among equal maxima, NaN and -inf
 // never win, 0xFFFFFFFF when nothing wins; blocks until the index is on the
 // host (src/cuda/argmax.cu:71-98). Throws std::invalid_argument for a null
-// pointer or a size outside [1, 2^32-1].
+// pointer or a size outside [1, 2^32-1], std::runtime_error if the device
+// collector timed out waiting for a workgroup (qk_argmax_workspace_check).
 uint32_t argmax(const float* logits, size_t vocabulary_size);
 
 // Superblock rows -> fp32 (src/cuda/embedding.cu:65-84).

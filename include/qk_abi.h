@@ -224,6 +224,15 @@ int qk_ffn_workspace_check(void *workspace, qk_stream_t stream);
  * (different streams) need separate workspaces. */
 size_t qk_argmax_workspace_size(void);
 
+/* QK_ERR_RUNTIME if an argmax call on this workspace since the last check
+ * stopped waiting for a workgroup's candidate (its collector waits at most
+ * 0.2 s for each: only a device that could not start a workgroup for that long
+ * gets there), and the index it wrote is invalid; the workspace is then
+ * cleared for the next call. Synchronizes `stream`. No counterpart in the
+ * reference, whose argmax reduces on the host (src/cuda/argmax.cu:89-97); for
+ * callers that keep a workspace across calls, as qk_ffn_workspace_check. */
+int qk_argmax_workspace_check(void *workspace, qk_stream_t stream);
+
 /* *result (device uint32) = the index of the largest of logits[0, count): the
  * lowest index among equal maxima; NaN and -inf never win; 0xFFFFFFFF if no
  * entry wins. Replaces kernels::argmax (include/Kernels.hpp:77,

@@ -79,6 +79,7 @@ _SIGNATURES = {
     "qk_ffn": [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _int, _c_void_p, _int, _i64, _i64,
                _c_void_p, _c_void_p, _i64, _c_void_p, _size, _c_void_p],
     "qk_ffn_workspace_check": [_c_void_p, _c_void_p],
+    "qk_argmax_workspace_check": [_c_void_p, _c_void_p],
     "qk_argmax_workspace_size": [],
     "qk_argmax": [_c_void_p, _i64, _c_void_p, _c_void_p, _size, _c_void_p],
     "qk_matmul_argmax": [_c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
@@ -425,6 +426,11 @@ def matmul_ws(x, w, qtype: int, K: int, N: int, y, M: int, workspace, workspace_
 
 def argmax_workspace_size() -> int:
     return int(load().qk_argmax_workspace_size())
+
+
+def argmax_workspace_check(workspace, stream=None) -> None:
+    """Raises QKError if an argmax call on `workspace` timed out (then clears it)."""
+    check(load().qk_argmax_workspace_check(_ptr(workspace), _stream_ptr(stream)))
 
 
 def argmax(logits, count: int, result, workspace, workspace_bytes: int, stream=None) -> None:

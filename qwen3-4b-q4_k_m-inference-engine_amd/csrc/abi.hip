@@ -535,6 +535,29 @@ int qk_ffn_workspace_check(void* workspace, qk_stream_t stream) {
 
 size_t qk_argmax_workspace_size(void) { return qk::argmax_workspace_bytes(); }
 
+int qk_argmax_workspace_check(void* workspace, qk_stream_t stream) {
+  if (!workspace) return fail(QK_ERR_INVALID_ARGUMENT, "argmax workspace must be non-null");
+  uint32_t flag = 0;
+  char* base = static_cast<char*>(workspace);
+  hipError_t error = hipMemcpyAsync(&flag, base + qk::argmax_timeout_offset(), sizeof(flag),
+                                    hipMemcpyDeviceToHost, as_stream(stream));
+  if (error == hipSuccess) error = hipStreamSynchronize(as_stream(stream));
+  if (error != hipSuccess) return hip_fail(error, "argmax workspace read failed");
+  if (flag == 0) return QK_OK;
+  // The late partial a timed-out collector skipped may have landed in its
+  // slot after the collector cleared it: the stream is idle now, so clear
+  // every slot and the word for the next call.
+  error = hipMemsetAsync(base, 0, qk::argmax_slots_bytes(), as_stream(stream));
+  const uint32_t zero = 0;
+  if (error == hipSuccess)
+    error = hipMemcpyAsync(base + qk::argmax_timeout_offset(), &zero, sizeof(zero), hipMemcpyHostToDevice,
+                           as_stream(stream));
+  if (error == hipSuccess) error = hipStreamSynchronize(as_stream(stream));
+  if (error != hipSuccess) return hip_fail(error, "argmax workspace reset failed");
+  return fail(QK_ERR_RUNTIME,
+              "argmax collector timed out waiting for a workgroup's candidate; the index of that call is invalid");
+}
+
 int qk_argmax(const float* logits, int64_t count, uint32_t* result, void* workspace,
               size_t workspace_bytes, qk_stream_t stream) {
   // src/cuda/argmax.cu:73-74

@@ -1,6 +1,8 @@
 // Standalone device argmax over fp32 logits (replaces kernels::argmax,
 // include/Kernels.hpp:77, src/cuda/argmax.cu:71-98, without its blocking copy
 // of per-SM candidates: the last workgroup writes the index to device memory).
+#include <cstddef>
+
 #include "argmax.hpp"
 #include "qk_launch.hpp"
 
@@ -25,6 +27,8 @@ __global__ __launch_bounds__(64 * kArgmaxWaves) void argmax_kernel(const float* 
 }  // namespace
 
 size_t argmax_workspace_bytes() { return sizeof(ArgmaxWorkspace); }
+size_t argmax_timeout_offset() { return offsetof(ArgmaxWorkspace, timeout); }
+size_t argmax_slots_bytes() { return sizeof(ArgmaxWorkspace::partial); }
 
 hipError_t launch_argmax(const float* logits, int64_t count, void* workspace, uint32_t* result,
                          hipStream_t stream) {

@@ -155,6 +155,9 @@ hipError_t launch_gemm_core_multi(const void* workspace, const qk_segment* segme
 
 // Bytes of the argmax workspace (zero-filled once by the caller).
 size_t argmax_workspace_bytes();
+// Byte offsets in that workspace of the timeout word and of the partial slots.
+size_t argmax_timeout_offset();
+size_t argmax_slots_bytes();
 
 // *result = argmax of logits[0, count) with the reference's rules.
 hipError_t launch_argmax(const float* logits, int64_t count, void* workspace, uint32_t* result,

@@ -115,6 +115,7 @@ uint32_t argmax(const float* logits, size_t vocabulary_size) {
                  "HIP kernel launch failed");
     uint32_t index = 0;
     check_status(qk_memcpy_d2h(&index, result.data, sizeof(index), nullptr), "HIP copy failed");
+    check_status(qk_argmax_workspace_check(workspace.data, nullptr), "HIP argmax failed");
     return index;
 }
 

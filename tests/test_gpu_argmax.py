@@ -38,6 +38,28 @@ def test_argmax_random(gpu, oracle, count):
         v = -v
 
 
+def test_argmax_workspace_check_reports_and_clears_a_timeout(gpu, oracle):
+    """The collector's bounded wait, when it gives up, sets a word after the
+    1024 partial slots (byte 8192) and writes an index without that partial;
+    qk_argmax_workspace_check reports it once and clears the word and every
+    slot (a late partial may have landed after the collector cleared its
+    slot). Planted from the host here (no workgroup is made to stall); a
+    stale slot planted with it must not reach the next call's index."""
+    ws, n = workspace(gpu)
+    gpu.argmax_workspace_check(ws)  # a zeroed workspace: nothing to report
+    ws.upload(np.array([1], np.uint32), offset=8192)
+    stale = np.zeros(2, np.uint64)
+    stale[1] = np.uint64(0xFFFFFFFFFFFFFFF0)  # slot 1: a huge key left over from a late publisher
+    ws.upload(stale, offset=0)
+    with pytest.raises(gpu.QKError, match="argmax collector timed out"):
+        gpu.argmax_workspace_check(ws)
+    assert not np.any(ws.download(np.uint32))
+    gpu.argmax_workspace_check(ws)
+    v = np.random.default_rng(5).standard_normal(151936).astype(np.float32)
+    assert run_argmax(gpu, ws, n, v) == oracle.argmax(v)
+    gpu.argmax_workspace_check(ws)
+
+
 def test_argmax_ties_nan_inf(gpu, oracle):
     ws, n = workspace(gpu)
     rng = np.random.default_rng(3)
