@@ -335,7 +335,8 @@ def prefill_gemm(qk, stream):
 
 
 def measure_configs(qk, sweep: DecodeSweep, stream):
-    """The other BASELINE configurations, reported beside the headline sweep."""
+    """The other workloads (single Q4_K / Q6_K mat-vecs, the FFN sweep, the
+    prefill GEMMs, the M = 8 decode sweep), reported beside the headline sweep."""
     out = {"0_q4k_gemv": single_gemv(qk, stream, Q4, 2560, 9728, 0),
            "1_q6k_gemv": single_gemv(qk, stream, Q6, 9728, 2560, 1)}
     separate = DecodeSweep(qk, M=1, weights_of=sweep, fused_ffn=False)
@@ -408,11 +409,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--no-roofline", action="store_true")
-    ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configurations")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other workloads")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the path shards over output rows with no per-mat-vec exchange; see DESIGN.md)",
+              "(the path would shard over output rows, with no exchange inside a mat-vec)",
               file=sys.stderr)
         return 2
 

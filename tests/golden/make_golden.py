@@ -14,7 +14,7 @@ in float (src/tests/reference/MatmulReference.hpp:31-39), plus a wide-range
 row; their Q8 round trip is round(x/amax*127)*(amax/127) in float with
 round-half-away-from-zero (MatmulReference.hpp:11-29), and the products are
 double sums of the round trip times the weights (MatmulReference.hpp:42-64).
-Rows include the closed-form cases of the survey: d = 1, dmin = 0, sc = 1 (w
+Rows include these closed-form cases: d = 1, dmin = 0, sc = 1 (w
 = q); sc = 0, dmin = 1, m = k (w = -k); the smallest fp16 subnormal d; Q6_K
 all-zero and all-ones codes (w = -32, w = 31); d = 0; negative int8 scales.
 

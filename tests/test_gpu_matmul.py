@@ -1,6 +1,6 @@
 """GPU parity of the HIP path against the CPU oracle, through the C-ABI.
 
-Bars: dequantized weights bit-exact; matmul outputs
+Bars (the path's stated tolerances): dequantized weights bit-exact; matmul outputs
 within max |y - y_ref| / ||y_ref[m,:]||_2 <= 1e-3 of the oracle's
 double-accumulated product. The reference's own per-element criterion,
 Catch2 Approx(eps=1e-4, margin=3e-5) (src/tests/reference/MatmulReference.hpp:71-78),

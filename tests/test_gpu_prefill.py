@@ -1,15 +1,18 @@
-"""GPU parity of the prefill path (M > 8 activation rows: MFMA GEMM on
-weights dequantised into LDS) against the CPU oracle, through the C-ABI.
+"""GPU parity of the prefill path (M > 8 activation rows: an MFMA GEMM whose
+weight operands are built from the superblocks in registers) against the CPU
+oracle, through the C-ABI.
 
-Bar: max |y - y_ref| / ||y_ref[m,:]||_2 <= 1e-3 against
+Bar (the path's stated tolerance): max |y - y_ref| / ||y_ref[m,:]||_2 <= 1e-3 against
 the oracle's product of the Q8 round trip of x with the fp32 dequantised
 weights (src/tests/reference/MatmulReference.hpp:42-64). At full Qwen3 sizes
 the double-precision reference is numpy's float64 product of the oracle's
 dequantised weights and Q8 round trip, the same sums in another order.
-The GEMM splits both operands into fp16 hi + lo (22 significant bits) and
-accumulates hi*hi + hi*lo + lo*hi in fp32, so it is held to the mat-vec
-path's tighter bars: row-norm error <= 1e-5 and the reference's per-element
-Approx (eps 1e-4, margin 3e-5) on at least 99% of the elements."""
+The GEMM splits the activations' Q8 round trip into fp16 hi + lo (22
+significant bits) against exact fp16 weight operands (sc*q; for Q6_K a
+rounded part plus an exact remainder) with fp32 accumulation, so it is held
+to the mat-vec path's tighter bars: row-norm error <= 1e-5 and the
+reference's per-element Approx (eps 1e-4, margin 3e-5) on at least 99% of
+the elements."""
 from __future__ import annotations
 
 import numpy as np
@@ -120,10 +123,10 @@ def test_prefill_activation_scale_invariance(gpu, oracle, qtype, scale):
                                    (300, 130, 768), (257, 3, 3328), (16, 64, 16640),
                                    (200, 20000, 512)])
 def test_prefill_ragged_against_oracle(gpu, oracle, qtype, M, N, K):
-    """Row and column counts off the tilings (Q4_K: 32 x 128 and, for grids
-    of 512+ tiles like 200 x 20000, 64 x 128; Q6_K: 128 x 64), narrow and odd
-    widths (K = 16640 takes the activation prep's two-pass path), against the
-    oracle's own double-accumulated product."""
+    """Row and column counts off the tilings (32 x 128, or 64 x 128 from 1.5
+    tiles per CU for Q4_K, as 200 x 20000 takes, and from half a tile per CU
+    for Q6_K), narrow and odd widths (K = 16640 takes the activation prep's
+    two-pass path), against the oracle's own double-accumulated product."""
     print(f"[case] type={qtype} M={M} N={N} K={K}", flush=True)
     w = make_weight(gpu, qtype, N, K, SEED + 20 + M + N)
     x = oracle.synth_normal(M * K, SEED + 2 + K)
