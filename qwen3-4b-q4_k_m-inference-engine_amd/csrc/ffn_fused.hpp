@@ -34,7 +34,8 @@
 // address to 32 (a single counter for 256 workgroups measured ~4 us from the
 // last arrival to the release; this scheme ~1.7 us on MI355X). The wait is
 // bounded: after spin_ticks of the 100 MHz real-time clock the workgroup sets
-// the timeout word and goes on (the outputs of that launch are then invalid).
+// the timeout word and goes on, writing NaN into its y rows (so a missed
+// check shows in the outputs; the launch's other rows may be invalid too).
 // Co-residency: the launcher sizes the grid to the CU count with LDS that
 // admits one workgroup per CU.
 #pragma once
@@ -227,8 +228,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
     issue_share<JG>(wsg, wsg.part ? p.up : p.gate, N, r0, S, BG, lane);
   }
   // Phase B share: superblocks of down rows [d0, d1) (row-major) for waves
-  // 0..14. The loads go out once the first half of the wave's gate/up chunks
-  // are in LDS (issued at entry they delayed the activations and the gate/up
+  // 0..14. The loads go out once all of the wave's gate/up chunks are in
+  // LDS (issued at entry they delayed the activations and the gate/up
   // bytes behind them). Wave 15's share is empty: its loads re-read the
   // activations' first 16 bytes, a cached line, so that its wait for its h
   // stores (which also waits for every earlier load of the wave) is not held
@@ -292,10 +293,15 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
   lds_f32* dsums = reinterpret_cast<lds_f32*>(dlds + kStreamWaves * JD * 1024);
   DownCodes<kEarly ? PD : 1> dc;
   const int npc = 4 * (wsd.sb_b - wsd.sb_a);
+  // the barrier's outcome for the whole workgroup, in phase A's norm
+  // partials (dead by now; phase B's regions are clear of them)
+  lds_u32* passed = reinterpret_cast<lds_u32*>(norm_part);
   if (wave == kHWave) {
-    // ---- grid barrier: h complete everywhere (this wave stored all of it)
-    __builtin_amdgcn_s_waitcnt(0);
-    if (lane == 0) (void)grid_barrier((global_u32*)(sync), last_epoch + 1u, spin);
+    // ---- grid barrier: h complete everywhere (this wave stored all of it).
+    // The wait is one inline-asm statement with a memory clobber, so the
+    // compiler keeps every h store before it and the counter add after it.
+    asm volatile("s_waitcnt vmcnt(0) expcnt(0) lgkmcnt(0)" ::: "memory");
+    if (lane == 0) *passed = grid_barrier((global_u32*)(sync), last_epoch + 1u, spin) ? 1u : 0u;
   } else if constexpr (kEarly) {
     // Meanwhile the down waves move their chunks to LDS and unpack their
     // pieces (nothing of that depends on h).
@@ -323,6 +329,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
     dc.s0 = (wsd.sb_a + (lane >> 2)) % Sd;  // superblock within its row of the first piece
   }
   __syncthreads();
+  // A timed-out wait read h that may be another call's: this workgroup's y
+  // rows become NaN (every other word of the outputs is still written).
+  const float y_scale = *passed ? 1.0f : __builtin_nanf("");
 
   // ---- phase B: Q8 of h into LDS, then the down rows
   const int nqh = min(kStreamWaves, (N / 8 + 64 * kXStaged - 1) / (64 * kXStaged));
@@ -360,11 +369,11 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
       float g = 0.0f;
       for (int t = k; t < Sd; t += 4) g += dsums[i * Sd + t];
       g = add_dpp<0x4E>(add_dpp<0xB1>(g));
-      if (k == 0) ((global_f32*)(yout))[d0 + i] = g;
+      if (k == 0) ((global_f32*)(yout))[d0 + i] = g * y_scale;
     }
   } else {
-    stream_consume<TD, JD, 0, false>(wsd, Sd, max_sbd, d0, d1, (global_f32*)(yout), nullptr, hq, dlds,
-                                     dsums, 1.0f);
+    stream_consume<TD, JD, 0, false, true>(wsd, Sd, max_sbd, d0, d1, (global_f32*)(yout), nullptr, hq, dlds,
+                                           dsums, y_scale);
   }
 }
 

@@ -154,6 +154,24 @@ __device__ __forceinline__ void issue_share(WaveShare<J>& ws, const uint8_t* w, 
 // waves that form the row totals. HOOK_AT: when >= 0
 // (non-IL only), hook() runs right after chunk HOOK_AT is in LDS (the fused
 // FFN issues its next loads there, once part of this share has arrived).
+// A row's total from its S superblock sums by one lane, in the order of a
+// quad's (lane k adds sums k, k+4, ... in order from 0; then the DPP sums
+// (s0 + s1) + (s2 + s3)), so both give the same bits.
+__device__ __forceinline__ float row_total_one_lane(const lds_f32* r, int S) {
+  float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+  int t = 0;
+  for (; t + 4 <= S; t += 4) {
+    s0 += r[t];
+    s1 += r[t + 1];
+    s2 += r[t + 2];
+    s3 += r[t + 3];
+  }
+  if (t < S) s0 += r[t];
+  if (t + 1 < S) s1 += r[t + 1];
+  if (t + 2 < S) s2 += r[t + 2];
+  return (s0 + s1) + (s2 + s3);
+}
+
 struct NoHook {
   __device__ __forceinline__ void operator()() const {}
 };
@@ -231,24 +249,31 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
   // Row totals, a quad per row: lane k of the quad adds the row's superblock
   // sums k, k+4, ... in order, then the quad's DPP sum.
   const int nrows = r1 - r0;
-  const int k = lane & 3;
   const int rt = static_cast<int>(threadIdx.x) - 64 * ROW_WAVE0;
-  const int first = rt >= 0 && rt < 64 * ROW_WAVES ? rt >> 2 : nrows;
   // When only some waves form the totals (the fused FFN, whose other waves go
-  // on to VALU-heavy work on the same SIMDs), they run at raised priority:
-  // sharing the SIMD evenly made one wave's 38 totals take ~2.5 us.
+  // on to VALU-heavy work on the same SIMDs), they run at raised priority
+  // (sharing the SIMD evenly made one wave's 38 totals take ~2.5 us), one lane
+  // per row, adding the row's sums in the quad order below.
   constexpr bool kPrio = ROW_WAVES < kStreamWaves;
+  const int k = kPrio ? 0 : lane & 3;
+  const int first = rt >= 0 && rt < 64 * ROW_WAVES ? (kPrio ? rt : rt >> 2) : nrows;
   if constexpr (kPrio) {
     if (first < nrows) __builtin_amdgcn_s_setprio(3);
   }
-  for (int i = first; i < nrows; i += 16 * ROW_WAVES) {
-    float g = 0.0f, u = 0.0f;
-    for (int t = k; t < S; t += 4) {
-      g += sums[i * S + t];
-      if constexpr (MODE == 1) u += sums[max_sb + i * S + t];
+  for (int i = first; i < nrows; i += (kPrio ? 64 : 16) * ROW_WAVES) {
+    float g, u = 0.0f;
+    if constexpr (kPrio) {
+      g = row_total_one_lane(sums + i * S, S);
+      if constexpr (MODE == 1) u = row_total_one_lane(sums + max_sb + i * S, S);
+    } else {
+      g = 0.0f;
+      for (int t = k; t < S; t += 4) {
+        g += sums[i * S + t];
+        if constexpr (MODE == 1) u += sums[max_sb + i * S + t];
+      }
+      g = add_dpp<0x4E>(add_dpp<0xB1>(g));
+      if constexpr (MODE == 1) u = add_dpp<0x4E>(add_dpp<0xB1>(u));
     }
-    g = add_dpp<0x4E>(add_dpp<0xB1>(g));
-    if constexpr (MODE == 1) u = add_dpp<0x4E>(add_dpp<0xB1>(u));
     if constexpr (SCALED) {
       g *= out_scale;
       u *= out_scale;
