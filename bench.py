@@ -84,8 +84,14 @@ class Op:
 class DecodeSweep:
     """Weights, activations and the per-token launch sequence of the decode sweep."""
 
-    def __init__(self, qk, M: int = 1, weights_of: "DecodeSweep | None" = None, fused_ffn: bool = True):
+    def __init__(self, qk, M: int = 1, weights_of: "DecodeSweep | None" = None, fused_ffn: bool = True,
+                 engine_calls: bool = False):
         self.qk, self.M = qk, M
+        # engine_calls: the reference engine's own per-layer sequence, unmodified
+        # (src/Engine.cpp:83-85,94,98-101,109-110): q, k, v, o, gate, up as
+        # separate kernels::matmul calls, silu_multiply, down, then the lm_head
+        # matmul into logits and argmax; no fused entry points
+        self.engine_calls = engine_calls
         # the FFN block through qk_ffn: M = 1 one launch (gate, up, SiLU*up,
         # down); M = 2..8 gate/up, one Q8 of h into the workspace, down on it
         self.fused_ffn = fused_ffn
@@ -112,6 +118,7 @@ class DecodeSweep:
         qk.synth_normal(self.x_ffn, M * 2560, SEED + 3)
         self.y = {n: buf(N) for n, _, _, N in LAYER}
         self.h = buf(9728)
+        self.gate, self.up = buf(9728), buf(9728)
         self.logits = buf(LM_HEAD[3])
         self.argmax_bytes = qk.argmax_workspace_size()
         self.argmax_ws = qk.DeviceBuffer(self.argmax_bytes)
@@ -129,6 +136,8 @@ class DecodeSweep:
         SiLU*up in one launch, ffn_down; then lm_head."""
         qk, M, y = self.qk, self.M, self.y
         out = []
+        if self.engine_calls:
+            return self.engine_ops(stream)
         for layer in self.layers:
             segs = [(layer[n], q, N, y[n]) for n, q, K, N in LAYER[:3]]
             out.append(Op("attn_qkv", sum(weight_bytes(q, 2560, N) for n, q, K, N in LAYER[:3])
@@ -158,6 +167,33 @@ class DecodeSweep:
         else:
             out.append(Op("lm_head", gemv_bytes(qtype, K, N, M),
                           lambda: qk.matmul(self.x_attn, self.lm_head, qtype, K, N, self.logits, M, stream)))
+        return out
+
+    def engine_ops(self, stream):
+        """The unmodified engine's launches per token: every projection its own
+        kernels::matmul (qk_matmul), SiLU*up in its own kernel, the logits
+        written out and reduced by qk_argmax."""
+        qk, M, y = self.qk, self.M, self.y
+        out = []
+        for layer in self.layers:
+            for n, q, K, N in LAYER[:3]:
+                out.append(Op("engine_matmul", gemv_bytes(q, K, N, M),
+                              lambda w=layer[n], q=q, K=K, N=N, n=n: qk.matmul(self.x_attn, w, q, K, N, y[n], M, stream)))
+            out.append(Op("engine_matmul", gemv_bytes(Q4, 4096, 2560, M),
+                          lambda w=layer["attn_output"]: qk.matmul(self.x_o, w, Q4, 4096, 2560, y["attn_output"], M,
+                                                                   stream)))
+            for n, dst in (("ffn_gate", self.gate), ("ffn_up", self.up)):
+                out.append(Op("engine_matmul", gemv_bytes(Q4, 2560, 9728, M),
+                              lambda w=layer[n], dst=dst: qk.matmul(self.x_ffn, w, Q4, 2560, 9728, dst, M, stream)))
+            out.append(Op("engine_silu", 3 * 4 * M * 9728,
+                          lambda: qk.silu_multiply(self.gate, self.up, self.h, M * 9728, stream)))
+            out.append(Op("engine_matmul", gemv_bytes(Q6, 9728, 2560, M),
+                          lambda w=layer["ffn_down"]: qk.matmul(self.h, w, Q6, 9728, 2560, y["ffn_down"], M, stream)))
+        name, qtype, K, N = LM_HEAD
+        out.append(Op("engine_matmul", gemv_bytes(qtype, K, N, M),
+                      lambda: qk.matmul(self.x_attn, self.lm_head, qtype, K, N, self.logits, M, stream)))
+        out.append(Op("engine_argmax", 4 * N + 4,
+                      lambda: qk.argmax(self.logits, N, self.next_token, self.argmax_ws, self.argmax_bytes, stream)))
         return out
 
     def bytes_per_step(self) -> int:
@@ -334,6 +370,44 @@ def prefill_gemm(qk, stream):
     return out
 
 
+PROMPT_M = 23  # the reference's published first-token prompt (README.md:30-37)
+
+
+def prefill_small_m(qk, sweep: DecodeSweep, stream, M: int = PROMPT_M):
+    """The projections of a short prompt's prefill (src/Engine.cpp:71-111 at
+    tokens = M): each shape over the sweep's 36 layers' distinct weights (the
+    lm_head repeated 8 times), one kernels::matmul per call with a caller
+    workspace, against the same shapes at M = 1. At this M the weights
+    dominate the bytes, so the rate is HBM GB/s."""
+    out = {}
+    xs = {K: qk.DeviceBuffer(4 * M * K) for K in (2560, 4096, 9728)}
+    for K, x in xs.items():
+        qk.synth_normal(x, M * K, SEED + 23 + K)
+    shapes = [(name, qtype, K, N, [layer[name] for layer in sweep.layers]) for name, qtype, K, N in LAYER]
+    name, qtype, K, N = LM_HEAD
+    shapes.append((name, qtype, K, N, [sweep.lm_head] * 8))
+    for name, qtype, K, N, ws in shapes:
+        y = qk.DeviceBuffer(4 * M * N)
+        need = max(qk.matmul_workspace_size(qtype, K, N, M), 16)
+        scratch = qk.DeviceBuffer(need)
+        qk.synchronize()
+        us_m = time_launches(qk, stream, [lambda w=w: qk.matmul_ws(xs[K], w, qtype, K, N, y, M, scratch, need, stream)
+                                          for w in ws])
+        launch = qk.last_launch()
+        us_1 = time_launches(qk, stream, [lambda w=w: qk.matmul(xs[K], w, qtype, K, N, y, 1, stream) for w in ws])
+        nbytes = gemv_bytes(qtype, K, N, M)
+        out[name] = {"shape": f"M={M} K={K} N={N} {'Q4_K' if qtype == Q4 else 'Q6_K'}", "kernel": launch,
+                     "avg_us": round(us_m, 3), "GB/s": round(nbytes / (us_m * 1e3), 1),
+                     "frac": round(nbytes / (us_m * 1e3) / PEAK_HBM_GBS, 4),
+                     "TFLOP/s": round(2 * M * N * K / (us_m * 1e6), 2),
+                     "m1_avg_us": round(us_1, 3), "ratio_to_m1": round(us_m / us_1, 3)}
+        y.free()
+        scratch.free()
+    for x in xs.values():
+        x.free()
+    return out
+
+
 def measure_configs(qk, sweep: DecodeSweep, stream):
     """The other workloads (single Q4_K / Q6_K mat-vecs, the FFN sweep, the
     prefill GEMMs, the M = 8 decode sweep), reported beside the headline sweep."""
@@ -349,6 +423,7 @@ def measure_configs(qk, sweep: DecodeSweep, stream):
                     "us_per_sweep": round(us, 1), "us_per_layer": round(us / 36, 2),
                     "GB/s": round(nbytes / (us * 1e3), 1), "frac": round(nbytes / (us * 1e3) / PEAK_HBM_GBS, 4)}
     out["3_prefill_gemm"] = prefill_gemm(qk, stream)
+    out["3_prefill_m23"] = prefill_small_m(qk, sweep, stream)
     sweep8 = DecodeSweep(qk, M=8, weights_of=sweep)
     graph = qk.Graph.capture(stream, lambda: sweep8.record(stream))
     ms = time_graph(qk, graph, stream, 2, 10)
@@ -359,31 +434,39 @@ def measure_configs(qk, sweep: DecodeSweep, stream):
     return out
 
 
+CPU_LAYERS = 8  # layers cycled by the CPU baseline: 8 x 64 MB, more than a host's L3
+
+
 def cpu_baseline(qk, sweep: DecodeSweep, budget_s: float):
-    """The CPU oracle (OpenMP, double accumulation) on a bounded sample: the
-    projections of layer 0, repeated until ~budget_s of CPU work."""
+    """The CPU oracle (OpenMP over output rows, double accumulation) on a
+    bounded sample of the same workload. One run = the 7 projections of one
+    layer at M = 1 (64 MB of weights); runs cycle over CPU_LAYERS distinct
+    layers so the host's caches do not hold the weights; one warm-up run,
+    then runs until ~budget_s, reported as the median run's rate."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import qk_oracle  # checker only: CPU baseline leg
 
     qk_oracle.load()
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
     rng_x = {K: qk_oracle.synth_normal(K, SEED + K) for K in (2560, 4096, 9728)}
-    weights = [(name, qtype, K, N, sweep.layers[0][name].download(np.uint8)) for name, qtype, K, N in LAYER]
-    done_bytes, elapsed, reps = 0, 0.0, 0
-    f32_bytes, f32_elapsed = 0, 0.0
-    while elapsed < budget_s or reps == 0:
-        for name, qtype, K, N, w in weights:
-            t0 = time.perf_counter()
-            qk_oracle.reference_product(rng_x[K], w, qtype, K, N, threads=threads)
-            elapsed += time.perf_counter() - t0
-            done_bytes += gemv_bytes(qtype, K, N, 1)
-        reps += 1
-    for name, qtype, K, N, w in weights:
+    layers = [[(qtype, K, N, sweep.layers[l][name].download(np.uint8)) for name, qtype, K, N in LAYER]
+              for l in range(CPU_LAYERS)]
+    run_bytes = sum(gemv_bytes(qtype, K, N, 1) for _, qtype, K, N in LAYER)
+
+    def run(l, product):
         t0 = time.perf_counter()
-        qk_oracle.reference_product_f32(rng_x[K], w, qtype, K, N, threads=threads)
-        f32_elapsed += time.perf_counter() - t0
-        f32_bytes += gemv_bytes(qtype, K, N, 1)
-    gbs = done_bytes / elapsed / 1e9
+        for qtype, K, N, w in layers[l % CPU_LAYERS]:
+            product(rng_x[K], w, qtype, K, N, threads=threads)
+        return time.perf_counter() - t0
+
+    run(0, qk_oracle.reference_product)  # warm-up
+    times, total = [], 0.0
+    while total < budget_s or len(times) < 5:
+        t = run(len(times) + 1, qk_oracle.reference_product)
+        times.append(t)
+        total += t
+    f32 = [run(l, qk_oracle.reference_product_f32) for l in range(1, 6)]
+    gbs = run_bytes / float(np.median(times)) / 1e9
     cpu = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -394,10 +477,12 @@ def cpu_baseline(qk, sweep: DecodeSweep, budget_s: float):
         pass
     return {
         "value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": f"oracle reference_product (Q8 round trip, dequant, double accumulation) of the "
-                  f"7 layer-0 projections at M=1, repeated {reps}x ({elapsed:.1f} s)",
+        "sample": f"oracle reference_product (Q8 round trip, dequant, double accumulation) of the 7 "
+                  f"projections of one layer at M=1 ({run_bytes / 1e6:.1f} MB), cycling over {CPU_LAYERS} "
+                  f"distinct layers; median of {len(times)} runs after 1 warm-up ({total:.1f} s)",
+        "runs": len(times), "min_run_GB/s": round(run_bytes / min(times) / 1e9, 3),
         "tokens_per_s": round(gbs * 1e9 / sweep.bytes_per_step(), 3),
-        "fp32_accumulation_GB/s": round(f32_bytes / f32_elapsed / 1e9, 3),
+        "fp32_accumulation_GB/s": round(run_bytes / float(np.median(f32)) / 1e9, 3),
         "cpu": cpu,
     }
 
@@ -440,6 +525,23 @@ def main() -> int:
     gbs = bytes_step / (ms * 1e-3) / 1e9
     log(f"graph step {ms:.4f} ms -> {gbs:.1f} GB/s, {1e3 / ms:.1f} tok/s (eager step {eager_ms:.2f} ms)")
 
+    # the same step through the unmodified engine's calls (no fused entry points)
+    dropin = DecodeSweep(qk, M=1, weights_of=sweep, engine_calls=True)
+    dgraph = qk.Graph.capture(stream, lambda: dropin.record(stream))
+    dropin_ms = time_graph(qk, dgraph, stream, args.warmup, args.steps)
+    dgraph.destroy()
+    log(f"drop-in (engine calls unchanged) step {dropin_ms:.4f} ms")
+    # the bounded waits of the timed replays (FFN grid barrier, argmax
+    # collector): each check reports and clears a timed-out wait
+    timeouts = 0
+    for ws, check in ((sweep.ffn_ws, qk.ffn_workspace_check), (sweep.argmax_ws, qk.argmax_workspace_check),
+                      (dropin.argmax_ws, qk.argmax_workspace_check)):
+        try:
+            check(ws, stream)
+        except qk.QKError as e:
+            timeouts += 1
+            log(f"timed-out wait reported: {e}")
+
     roofline, kernels = None, None
     if not args.no_roofline:
         kernels = kernel_roofline(qk, sweep, stream)
@@ -476,6 +578,10 @@ def main() -> int:
                                "+ lm_head 151936x2560 Q6_K with next-token argmax, Q8 activations, "
                                "3 launches/layer (qkv, o, FFN block) + 1, graph-replayed",
                    "tokens_per_s": round(1e3 / ms, 2), "bytes_per_step": bytes_step,
+                   "dropin_ms_per_step": round(dropin_ms, 5),
+                   "dropin_note": "the same step through the engine's unmodified calls (src/Engine.cpp:83-110): "
+                                  "9 qk_matmul + qk_silu_multiply per layer, lm_head qk_matmul + qk_argmax",
+                   "barrier_timeouts": timeouts,
                    "frac_of_peak_hbm": round(gbs / PEAK_HBM_GBS, 4), "eager_ms_per_step": round(eager_ms, 3),
                    "device": info["name"], "arch": info["arch"]},
         "roofline": roofline,

@@ -84,11 +84,12 @@ def test_other_validation(qk):
     assert lib.qk_quantize_q8(None, 1, 100, None, None) == 1
     assert lib.qk_matmul_workspace_size(12, 2560, 8, 3) == 0  # Q8 runs inside the kernel
     # M > 8: two fp16 planes (hi, lo) of M x K plus M row scales, rounded up to 256
-    # 9*2560*4 + 36 (hi/lo planes, row scales) -> 92208, + 9*10*32 sub-block sums -> 372*256
-    # (K = 2560 is too shallow to split)
-    assert lib.qk_matmul_workspace_size(12, 2560, 8, 9) == 95232
-    # one tile of K = 4096 (16 superblocks): split 2 ways -> 152320 + 2 x 9 x 8 fp32 partials
-    assert lib.qk_matmul_workspace_size(12, 4096, 8, 9) == 153088
+    # 9*2560*4 + 36 (hi/lo planes, row scales) -> 92208, + 9*10*32 sub-block sums -> 372*256;
+    # M <= 32 splits K down to single superblocks (one tile: 10 splits) -> + 10 x 9 x 8 fp32
+    # partials -> 98112, rounded up to 384*256
+    assert lib.qk_matmul_workspace_size(12, 2560, 8, 9) == 98304
+    # one tile of K = 4096 (16 superblocks): 16 splits -> 152320 + 16 x 9 x 8 fp32 partials
+    assert lib.qk_matmul_workspace_size(12, 4096, 8, 9) == 156928
     assert lib.qk_matmul_workspace_size(14, 256, 8, 11) == 11776  # 11*256*4 + 44 -> 11312, + 11*32 -> 46*256
     assert lib.qk_matmul_workspace_size(14, 2500, 8, 11) == 0  # rejected shape
     p = ctypes.c_void_p(256)

@@ -217,7 +217,7 @@ def run_model(cfg, oracle, qtype, M, N, K, seed, splits=1):
 
 @pytest.mark.parametrize("qtype", [12, 14])
 @pytest.mark.parametrize("TM,TN", [(2, 1), (1, 1)])  # the two tiles the launcher uses
-@pytest.mark.parametrize("K,splits", [(768, 1), (1024, 3)])
+@pytest.mark.parametrize("K,splits", [(768, 1), (1024, 3), (1280, 5)])
 def test_gemm_model_matches_oracle(oracle, qtype, TM, TN, K, splits):
     y, ref = run_model(Cfg(TM, TN), oracle, qtype, M=70, N=300, K=K, seed=91, splits=splits)
     err = oracle.row_norm_error(y, ref)

@@ -218,9 +218,14 @@ def batch_weight(qk, oracle, name):
     return _BATCH_WEIGHTS[name]
 
 
-@pytest.mark.parametrize("name", ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate",
-                                  "ffn_down", "lm_head"])
-@pytest.mark.parametrize("M", [2, 4, 8])
+BATCHED_CASES = ([(name, M) for name in ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_down",
+                                          "lm_head"] for M in (2, 4, 8)]
+                 # partly filled matrix-core tiles: a Q6_K second row half (MH = 2) and
+                 # Q4_K diagonal tiles with rows at or above M
+                 + [(name, M) for name in ["attn_q", "attn_v", "ffn_down"] for M in (3, 6, 7)])
+
+
+@pytest.mark.parametrize("name,M", BATCHED_CASES)
 def test_matmul_batched_qwen3_shapes(gpu, oracle, name, M):
     """Batched decode (M = 2..8, the rows src/Engine.cpp:83-109 pass per step
     when several sequences decode together) at every full Qwen3 shape. The
@@ -331,18 +336,20 @@ def test_matmul_entry_points_agree_bitwise(gpu, oracle, qtype):
     assert oracle.row_norm_error(c, a.astype(np.float64)) <= 1e-6
 
 
-@pytest.mark.parametrize("M", [1, 3, 8, 11])
-def test_matmul_segments_qkv(gpu, oracle, M):
-    """attn q/k/v of one input in one launch (Q4_K, Q4_K, Q6_K mixed)."""
+@pytest.mark.parametrize("M,v_type", [(1, Q6), (3, Q6), (8, Q6), (11, Q6), (1, Q4), (3, Q4), (8, Q4)])
+def test_matmul_segments_qkv(gpu, oracle, M, v_type):
+    """attn q/k/v of one input in one launch: the two layer types of a
+    Q4_K_M file (attn_v in Q6_K, and in Q4_K on the layers that keep it at 4
+    bits, where every segment shares one weight type)."""
     K = 2560
-    shapes = [(Q4, 4096), (Q4, 1024), (Q6, 1024)]
+    shapes = [(Q4, 4096), (Q4, 1024), (v_type, 1024)]
     ws = [make_weight(gpu, oracle, q, N, K, SEED + 600 + i) for i, (q, N) in enumerate(shapes)]
     x = oracle.synth_normal(M * K, SEED + 601)
     xd = gpu.DeviceBuffer.from_array(x)
     ys = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes]
     gpu.matmul_segments(xd, M, K, [(w, q, N, y) for w, (q, N), y in zip(ws, shapes, ys)])
     gpu.synchronize()
-    print(f"[case] qkv M={M} launch {gpu.last_launch()}", flush=True)
+    print(f"[case] qkv M={M} v_type={v_type} launch {gpu.last_launch()}", flush=True)
     for w, (q, N), y in zip(ws, shapes, ys):
         got = y.download(np.float32).reshape(M, N)
         ref = oracle.reference_product(x, w.download(np.uint8), q, K, N)
@@ -484,8 +491,8 @@ def test_prologue_quantisation_bitwise(gpu, oracle, M, K):
     assert bad[0].size == 0, f"{bad[0].size} mismatches, first at (m, k) = ({bad[0][0]}, {bad[1][0]})"
 
 
-@pytest.mark.parametrize("name", ["attn_q", "attn_v", "attn_output", "ffn_gate"])
-@pytest.mark.parametrize("M", [2, 8])
+@pytest.mark.parametrize("name,M", [(name, M) for name in ["attn_q", "attn_v", "attn_output", "ffn_gate"]
+                                    for M in (2, 8)] + [("attn_q", 7), ("attn_v", 7)])
 def test_matmul_q8_batched_qwen3_shapes(gpu, oracle, name, M):
     """qk_quantize_q8 + qk_matmul_q8 (the caller-quantised input of
     src/cuda/matmul.cu's two launches) at M = 2 and 8 on the full Qwen3

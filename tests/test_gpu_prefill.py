@@ -77,6 +77,34 @@ def test_prefill_qwen3_shapes_m512(gpu, oracle, name, qtype, K, N):
     check(oracle, got, ref, name)
 
 
+PROMPT_SHAPES = PREFILL + [("lm_head", Q6, 2560, 151936)]
+
+
+@pytest.mark.parametrize("name,qtype,K,N", PROMPT_SHAPES)
+def test_prefill_qwen3_shapes_m23(gpu, oracle, name, qtype, K, N):
+    """The reference's own prompt length (README.md:30-37: a 23-token
+    templated prompt, src/Engine.cpp:71-111 with tokens = 23) on every Qwen3
+    projection shape and the lm_head, through kernels::matmul, allocating and
+    with a caller workspace (same bits)."""
+    M = 23
+    w = make_weight(gpu, qtype, N, K, SEED + 30 + PROMPT_SHAPES.index((name, qtype, K, N)))
+    x = oracle.synth_normal(M * K, SEED + 3)
+    xd = gpu.DeviceBuffer.from_array(x)
+    y = gpu.DeviceBuffer(4 * M * N)
+    gpu.matmul(xd, w, qtype, K, N, y, M)
+    gpu.synchronize()
+    print(f"[case] {name} type={qtype} K={K} N={N} M={M} launch {gpu.last_launch()}", flush=True)
+    got = y.download(np.float32).reshape(M, N)
+    ref = float64_reference(oracle, x, w.download(np.uint8), qtype, K, N, M)
+    check(oracle, got, ref, name)
+    need = gpu.matmul_workspace_size(qtype, K, N, M)
+    ws = gpu.DeviceBuffer(max(need, 16))
+    y2 = gpu.DeviceBuffer(4 * M * N)
+    gpu.matmul_ws(xd, w, qtype, K, N, y2, M, ws, need)
+    gpu.synchronize()
+    assert np.array_equal(y2.download(np.float32).reshape(M, N), got)
+
+
 @pytest.mark.parametrize("qtype", [Q4, Q6])
 def test_prefill_single_column_ill_conditioned(gpu, oracle, qtype):
     """N = 1: the row norm is one |y| value, which cancellation can bring near
