@@ -200,8 +200,11 @@ size_t qk_ffn_workspace_size(void);
  * reads h back, quantises it and runs the down rows, whose weights were
  * loaded during phase 1. That launch needs every workgroup resident at once:
  * do not overlap it with other kernels on the device. Its barrier wait is
- * bounded: if it ever times out, the outputs of that call are invalid and
- * qk_ffn_workspace_check reports it. M = 2..8 (when M*N/32 Q8 blocks fit in
+ * bounded: if it ever times out, the workgroups that gave up write NaN into
+ * their y rows, the outputs of that call are invalid, and
+ * qk_ffn_workspace_check reports it (an engine that graph-replays decode steps
+ * checks after each replay of a step, or at least before it trusts a token).
+ * M = 2..8 (when M*N/32 Q8 blocks fit in
  * 160 KiB, M*K norm rows in 512 KiB and M rows of Q8(h) in one down launch):
  * the norm into the workspace, qk_ffn_gate_up, h quantised once into the
  * workspace, then the down mat-vec on those Q8 blocks; nothing is allocated.
@@ -227,8 +230,11 @@ size_t qk_argmax_workspace_size(void);
 /* QK_ERR_RUNTIME if an argmax call on this workspace since the last check
  * stopped waiting for a workgroup's candidate (its collector waits at most
  * 0.2 s for each: only a device that could not start a workgroup for that long
- * gets there), and the index it wrote is invalid; the workspace is then
- * cleared for the next call. Synchronizes `stream`. No counterpart in the
+ * gets there): the index that call wrote is invalid, and so may be the index
+ * of every later call on the workspace until this check, since the late
+ * candidate can land in its slot after the collector cleared it and be taken
+ * by the next call as its own. The check clears every slot, so the next call
+ * is sound again. Synchronizes `stream`. No counterpart in the
  * reference, whose argmax reduces on the host (src/cuda/argmax.cu:89-97); for
  * callers that keep a workspace across calls, as qk_ffn_workspace_check. */
 int qk_argmax_workspace_check(void *workspace, qk_stream_t stream);
