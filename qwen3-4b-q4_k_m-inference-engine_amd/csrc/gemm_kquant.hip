@@ -545,10 +545,11 @@ struct KQPlan {
 // below (attn_q/k, attn_output at M = 512); Q6_K, whose stages cost more,
 // takes 64 x 128 from half a tile per CU (ffn_down) and 32 x 128 below
 // (attn_v). The tile height does not change any output element's sums. Grids of fewer than two
-// tiles per CU split a deep K (at most 4 ways, at least 8 superblocks a
-// split) so that about two work units reach every CU; a reduce kernel adds
-// the splits. Measured at M = 512: ffn_down (K = 9728, 3 splits) 102 us
-// with its reduce against 137; at K = 2560 the reduce (~5 us) ate the gain.
+// tiles per CU split K (at most 4 ways, at least 4 superblocks a split) so
+// that about two work units reach every CU; a reduce kernel adds the splits.
+// Measured at M = 512: ffn_down (K = 9728, 3 splits) 102 us with its reduce
+// against 137; attn_k / attn_v alone (K = 2560, 128 tiles, 2 splits of 5
+// superblocks) 26.3 -> 22.4 us and 33.3 -> 27.1 us.
 // At M <= 32 (one row of tiles: a short prompt) K splits down to single
 // superblocks. Measured at M = 23 (graph replays over 36 distinct layers,
 // prep and reduce included): ffn_gate 27.1 -> 20.8 us, attn_k 23.1 -> 12.7,
@@ -567,7 +568,7 @@ KQPlan plan(int type, int64_t M, int64_t N, int64_t K) {
   const bool short_m = M <= 32;
   const int64_t by_grid = short_m ? std::clamp<int64_t>((2 * kPlanCUs + tiles - 1) / tiles, 1, K / 256)
                                   : std::clamp<int64_t>(2 * kPlanCUs / tiles, 1, 4);
-  const int64_t by_depth = short_m ? K / 256 : std::max<int64_t>(K / 256 / 8, 1);
+  const int64_t by_depth = short_m ? K / 256 : std::max<int64_t>(K / 256 / 4, 1);
   // (fewer than 512 tiles also keeps M below 16384, inside the reduce grid's
   // 65535 rows; the check states it)
   const bool fits_reduce = M <= 65535;
@@ -622,11 +623,12 @@ hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, cons
                                 hipStream_t stream, bool& launched) {
   launched = false;
   if (count < 2 || count > kKQMaxSegments) return hipSuccess;
-  // One launch when every matrix would run unsplit in its own launch: each
-  // tile then does exactly the work of its own launch (outputs bit for bit
-  // the same: the tile height changes no output element's sums), in one grid
-  // that fills the CUs. Q6_K matrices first: their tiles take longer, so they
-  // start first.
+  // One launch when the combined grid needs no split of K: each tile then
+  // does exactly the work of an unsplit launch of its matrix (outputs bit for
+  // bit those of the single launch when that does not split; within the
+  // splits' rounding of it otherwise: a split changes the order of the sums),
+  // in one grid that fills the CUs. Q6_K matrices first: their tiles take
+  // longer, so they start first.
   int order[kKQMaxSegments], n = 0;
   bool q4 = false, q6 = false;
   int64_t total = 0;
@@ -634,13 +636,13 @@ hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, cons
     for (int j = 0; j < count; ++j)
       if ((segments[j].type == QK_TYPE_Q6_K) == (pass == 0)) order[n++] = j;
   for (int j = 0; j < count; ++j) {
-    if (!gemm_kq_fits(M, K, segments[j].N) || plan(segments[j].type, M, segments[j].N, K).splits > 1)
-      return hipSuccess;
+    if (!gemm_kq_fits(M, K, segments[j].N)) return hipSuccess;
     (segments[j].type == QK_TYPE_Q4_K ? q4 : q6) = true;
     total += segments[j].N;
   }
   if (!gemm_kq_fits(M, K, total)) return hipSuccess;
   const int type = q4 && q6 ? 0 : q4 ? QK_TYPE_Q4_K : QK_TYPE_Q6_K;
+  if (plan(type == 0 ? QK_TYPE_Q4_K : type, M, total, K).splits > 1) return hipSuccess;
   // The tile shape of the combined grid. The mixed-type kernel exists for
   // 32 x 128 tiles only: it is taken while the grid has fewer than two
   // 64 x 128 tiles per CU (q + k + v at M = 512: 384), else same-type pairs run.

@@ -254,22 +254,32 @@ def test_prefill_entry_points_agree_bitwise(gpu, oracle, qtype):
 ])
 def test_prefill_segments_pairs_match_single_launches(gpu, oracle, M, K, shapes):
     """qk_matmul_segments at M > 8 runs its matrices in one GEMM launch when
-    none needs a split K (each workgroup takes its matrix's type), otherwise
-    same-type pairs or single launches: every output equals its
-    single-matrix qk_matmul bit for bit, and the oracle within the bar."""
+    the combined grid needs no split K (each workgroup takes its matrix's
+    type), otherwise same-type pairs or single launches. Every output equals
+    its single-matrix qk_matmul bit for bit when that launch does not split K
+    (the same tiles, the same sums); when it does (attn k / v alone at
+    M = 512), the two differ only by the order of fp32 sums: within 1e-6 of
+    the row norm. Both within the bar of the oracle."""
     ws = [make_weight(gpu, q, N, K, SEED + 60 + i) for i, (q, N) in enumerate(shapes)]
     x = oracle.synth_normal(M * K, SEED + 61)
     xd = gpu.DeviceBuffer.from_array(x)
     ys = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes]
     gpu.matmul_segments(xd, M, K, [(w, q, N, y) for w, (q, N), y in zip(ws, shapes, ys)])
     print(f"[case] segments M={M} K={K} {shapes} last launch {gpu.last_launch()}", flush=True)
-    singles = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes]
+    singles, split = [gpu.DeviceBuffer(4 * M * N) for _, N in shapes], []
     for w, (q, N), y in zip(ws, shapes, singles):
         gpu.matmul(xd, w, q, K, N, y, M)
+        launch = gpu.last_launch()  # gemm_kq_kernel<type,TM,TN,splits> grid=G
+        split.append(int(launch.split(">")[0].split(",")[-1]) > 1)
+        print(f"[case] single N={N} launch {launch}", flush=True)
     gpu.synchronize()
-    for w, (q, N), y, y1 in zip(ws, shapes, ys, singles):
+    for w, (q, N), y, y1, sp in zip(ws, shapes, ys, singles, split):
         got = y.download(np.float32)
-        assert np.array_equal(got, y1.download(np.float32))
+        one = y1.download(np.float32)
+        if sp:
+            assert oracle.row_norm_error(got.reshape(M, N), one.reshape(M, N).astype(np.float64)) <= 1e-6
+        else:
+            assert np.array_equal(got, one)
         if N <= 1024:
             ref = float64_reference(oracle, x, w.download(np.uint8), q, K, N, M)
             check(oracle, got.reshape(M, N), ref, f"segments q{q} N={N}")
