@@ -502,17 +502,28 @@ __global__ __launch_bounds__(64 * kWaves, TYPE == QK_TYPE_Q6_K ? 2 : 3) void gem
 }
 
 // y[m][n] = (partial 0 + partial 1 + ...) * 2^-s(m), the splits added in
-// order (results do not depend on timing). Grid (ceil(N / 256), M).
+// order (results do not depend on timing). Grid (ceil(N / 256), M). The
+// partials were written on every XCD and miss this one's L2, so each thread
+// has 16 splits' loads in flight at once (indices past the last re-read it)
+// instead of one load per dependent add.
 __global__ __launch_bounds__(256) void gemm_kq_reduce_kernel(const float* __restrict__ part,
                                                              const float* __restrict__ row_scale,
                                                              float* __restrict__ y, int M, int N,
                                                              int splits) {
+  constexpr int kBatch = 16;
   const int m = static_cast<int>(blockIdx.y);
   const int n = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
   if (n >= N) return;
   const int64_t at = static_cast<int64_t>(m) * N + n, plane = static_cast<int64_t>(M) * N;
-  float v = part[at];
-  for (int k = 1; k < splits; ++k) v += part[k * plane + at];
+  float v = 0.0f;
+  for (int k0 = 0; k0 < splits; k0 += kBatch) {
+    float p[kBatch];
+#pragma unroll
+    for (int kk = 0; kk < kBatch; ++kk) p[kk] = part[min(k0 + kk, splits - 1) * plane + at];
+#pragma unroll
+    for (int kk = 0; kk < kBatch; ++kk)
+      if (k0 + kk < splits) v = k0 + kk == 0 ? p[kk] : v + p[kk];
+  }
   y[at] = v * row_scale[m];
 }
 

@@ -319,6 +319,38 @@ def test_prefill_graph_replay_with_workspace(gpu, oracle):
     stream.destroy()
 
 
+def test_split_k_workspace_from_garbage_and_across_plans(gpu, oracle):
+    """Launches that split K keep their partial products in the workspace and
+    a reduce launch adds them in split order. A workspace that starts as 0xFF
+    bytes, reused by calls of different split plans one after another (10, 26
+    and 10 splits at M = 23; 2 and 3 at M = 512), gives the bits of a fresh
+    allocation every time: nothing read is left over from an earlier call."""
+    qk = gpu
+    shapes = [(23, "attn_k", Q4, 2560, 1024), (23, "ffn_down", Q6, 9728, 2560),
+              (23, "attn_v", Q6, 2560, 1024), (512, "attn_k", Q4, 2560, 1024),
+              (512, "ffn_down", Q6, 9728, 2560)]
+    need = max(qk.matmul_workspace_size(q, K, N, M) for M, _, q, K, N in shapes)
+    ws = qk.DeviceBuffer.from_array(np.full(need, 0xFF, np.uint8))
+    cases = []
+    for i, (M, name, q, K, N) in enumerate(shapes):
+        w = make_weight(qk, q, N, K, SEED + 60 + i)
+        xd = qk.DeviceBuffer.from_array(oracle.synth_normal(M * K, SEED + 61 + i))
+        y = qk.DeviceBuffer(4 * M * N)
+        qk.matmul(xd, w, q, K, N, y, M)
+        qk.synchronize()
+        cases.append((M, name, q, K, N, w, xd, y.download(np.float32)))
+        print(f"[case] {name} M={M} launch {qk.last_launch()}", flush=True)
+    for rep in range(2):
+        for M, name, q, K, N, w, xd, fresh in cases:
+            y = qk.DeviceBuffer(4 * M * N)
+            qk.matmul_ws(xd, w, q, K, N, y, M, ws, need)
+            qk.synchronize()
+            assert np.array_equal(y.download(np.float32), fresh), f"{name} M={M} pass {rep}"
+    M, name, q, K, N, w, xd, fresh = cases[0]
+    ref = float64_reference(oracle, xd.download(np.float32), w.download(np.uint8), q, K, N, M)
+    check(oracle, fresh.reshape(M, N), ref, f"{name} M={M}")
+
+
 @pytest.mark.parametrize("qtype,K,N,M", [(Q4, 2560, 9728, 64), (Q6, 9728, 2560, 40)])
 def test_ffn_gate_up_workspace_variant_and_deep_k(gpu, oracle, qtype, K, N, M):
     """qk_ffn_gate_up_ws equals qk_ffn_gate_up bit for bit; the deep-K shape
