@@ -333,9 +333,14 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
   // rows become NaN (every other word of the outputs is still written).
   const float y_scale = *passed ? 1.0f : __builtin_nanf("");
 
-  // ---- phase B: Q8 of h into LDS, then the down rows
-  const int nqh = min(kStreamWaves, (N / 8 + 64 * kXStaged - 1) / (64 * kXStaged));
-  if (wave < nqh) {
+  // ---- phase B: Q8 of h into LDS, then the down rows. Every wave takes
+  // quantiser tasks (lane l of the workgroup tasks l, l + 1024): with the
+  // fewest waves that stage all N / 8 tasks (10 for N = 9728, 2 tasks a lane)
+  // one SIMD ran 6 tasks a lane, with all 16 at most 5 (block 15.6-15.8 ->
+  // 15.5 us); phase A keeps its few quantiser waves, whose loads go out
+  // ahead of the weight loads (all 16 there measured slower).
+  constexpr int nqh = kStreamWaves;
+  {
     XStage<1> hs;
     stage_h(hout, N, nqh, hs);
     quantize_staged_into_lds<1>(1, N, nqh, hs, hq);  // N <= kStreamMaxK: all staged

@@ -408,9 +408,12 @@ def check_ffn(K, N, down_type, bases):
         # row totals of phase A by the first H_WAVES waves, a quad per row
         assert (r1 - r0) <= 10_000
     assert np.all(seen == 1) and np.all(seen_d == 1), "every superblock exactly once"
-    # h staging: every task of 8 values staged by nqh waves, 2 tasks per lane
-    nqh = min(WAVES, -(-(N // 8) // (64 * XSTAGED)))
-    assert 64 * nqh * XSTAGED >= N // 8
+    # h staging: all 16 waves stage tasks l, l + 1024 (lane l of the
+    # workgroup); every task of 8 values is staged, and the buffer range of
+    # the loads (N floats) makes the tasks past N / 8 read zeros
+    nqh = WAVES
+    t = np.arange(64 * nqh)[:, None] + 64 * nqh * np.arange(XSTAGED)[None, :]
+    assert np.array_equal(np.sort(t[t < N // 8]), np.arange(N // 8))
     # LDS: phase A (Q8 of x, wave regions, both parts' sums, norm partials);
     # phase B (Q8 of h, wave regions, sums) reuse the same bytes
     assert S * 8 * 48 + WAVES * JG * 1024 + 2 * max_sb * 4 + 4 * WAVES <= lds <= MAX_LDS
