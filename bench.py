@@ -408,29 +408,40 @@ def prefill_small_m(qk, sweep: DecodeSweep, stream, M: int = PROMPT_M):
     return out
 
 
-def measure_configs(qk, sweep: DecodeSweep, stream):
+CONFIG_PARTS = ("gemv", "ffn", "prefill", "m23", "m8")
+
+
+def measure_configs(qk, sweep: DecodeSweep, stream, only=None):
     """The other workloads (single Q4_K / Q6_K mat-vecs, the FFN sweep, the
-    prefill GEMMs, the M = 8 decode sweep), reported beside the headline sweep."""
-    out = {"0_q4k_gemv": single_gemv(qk, stream, Q4, 2560, 9728, 0),
-           "1_q6k_gemv": single_gemv(qk, stream, Q6, 9728, 2560, 1)}
-    separate = DecodeSweep(qk, M=1, weights_of=sweep, fused_ffn=False)
-    for key, src, fams in (("2_ffn_block_sweep", sweep, ("ffn_block",)),
-                           ("2_ffn_block_sweep_two_launches", separate, ("ffn_gate_up", "ffn_down"))):
-        ffn = [op for op in src.ops(stream) if op.family in fams]
-        us = time_launches(qk, stream, [op.call for op in ffn]) * len(ffn)
-        nbytes = sum(op.nbytes for op in ffn)
-        out[key] = {"shape": f"36 x (gate+up SiLU, down), M=1, {len(ffn) // 36} launch(es) per layer",
-                    "us_per_sweep": round(us, 1), "us_per_layer": round(us / 36, 2),
-                    "GB/s": round(nbytes / (us * 1e3), 1), "frac": round(nbytes / (us * 1e3) / PEAK_HBM_GBS, 4)}
-    out["3_prefill_gemm"] = prefill_gemm(qk, stream)
-    out["3_prefill_m23"] = prefill_small_m(qk, sweep, stream)
-    sweep8 = DecodeSweep(qk, M=8, weights_of=sweep)
-    graph = qk.Graph.capture(stream, lambda: sweep8.record(stream))
-    ms = time_graph(qk, graph, stream, 2, 10)
-    graph.destroy()
-    out["4_decode_sweep_m8"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(8e3 / ms, 1),
-                                "GB/s": round(sweep8.bytes_per_step() / (ms * 1e6), 1),
-                                "kernels": kernel_roofline(qk, sweep8, stream)}
+    prefill GEMMs, the M = 8 decode sweep), reported beside the headline sweep;
+    `only` names one part of CONFIG_PARTS (for a profiler run of that part)."""
+    out = {}
+    run = lambda part: only is None or only == part
+    if run("gemv"):
+        out["0_q4k_gemv"] = single_gemv(qk, stream, Q4, 2560, 9728, 0)
+        out["1_q6k_gemv"] = single_gemv(qk, stream, Q6, 9728, 2560, 1)
+    if run("ffn"):
+        separate = DecodeSweep(qk, M=1, weights_of=sweep, fused_ffn=False)
+        for key, src, fams in (("2_ffn_block_sweep", sweep, ("ffn_block",)),
+                               ("2_ffn_block_sweep_two_launches", separate, ("ffn_gate_up", "ffn_down"))):
+            ffn = [op for op in src.ops(stream) if op.family in fams]
+            us = time_launches(qk, stream, [op.call for op in ffn]) * len(ffn)
+            nbytes = sum(op.nbytes for op in ffn)
+            out[key] = {"shape": f"36 x (gate+up SiLU, down), M=1, {len(ffn) // 36} launch(es) per layer",
+                        "us_per_sweep": round(us, 1), "us_per_layer": round(us / 36, 2),
+                        "GB/s": round(nbytes / (us * 1e3), 1), "frac": round(nbytes / (us * 1e3) / PEAK_HBM_GBS, 4)}
+    if run("prefill"):
+        out["3_prefill_gemm"] = prefill_gemm(qk, stream)
+    if run("m23"):
+        out["3_prefill_m23"] = prefill_small_m(qk, sweep, stream)
+    if run("m8"):
+        sweep8 = DecodeSweep(qk, M=8, weights_of=sweep)
+        graph = qk.Graph.capture(stream, lambda: sweep8.record(stream))
+        ms = time_graph(qk, graph, stream, 2, 10)
+        graph.destroy()
+        out["4_decode_sweep_m8"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(8e3 / ms, 1),
+                                    "GB/s": round(sweep8.bytes_per_step() / (ms * 1e6), 1),
+                                    "kernels": kernel_roofline(qk, sweep8, stream)}
     return out
 
 
@@ -495,6 +506,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the other workloads")
+    ap.add_argument("--only-config", choices=CONFIG_PARTS,
+                    help="run only this part of the other workloads and print its results (no headline line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -509,6 +522,10 @@ def main() -> int:
     sweep = DecodeSweep(qk, M=1)
     log(f"weights ready ({sweep.bytes_per_step() / 1e9:.3f} GB/step) in {time.perf_counter() - t0:.1f} s")
     stream = qk.Stream()
+    if args.only_config:
+        print(json.dumps({"configs": measure_configs(qk, sweep, stream, only=args.only_config)}), flush=True)
+        stream.destroy()
+        return 0
 
     # eager step (host-enqueued launch by launch), for reference
     sweep.record(stream)
