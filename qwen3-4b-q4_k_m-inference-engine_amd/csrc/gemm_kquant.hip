@@ -570,7 +570,9 @@ constexpr int64_t kPlanCUs = 256;
 KQPlan plan(int type, int64_t M, int64_t N, int64_t K) {
   const int64_t tiles64 = ((M + 63) / 64) * ((N + 127) / 128);
   const int64_t tiles32 = ((M + 31) / 32) * ((N + 127) / 128);
-  const bool wide = type == QK_TYPE_Q6_K ? 2 * tiles64 >= kPlanCUs : 2 * tiles64 >= 3 * kPlanCUs;
+  // (M <= 32: one row of tiles either way, and a 64-row tile would compute
+  // its padding rows: the lm_head at M = 23 is 1187 tiles of either height)
+  const bool wide = M > 32 && (type == QK_TYPE_Q6_K ? 2 * tiles64 >= kPlanCUs : 2 * tiles64 >= 3 * kPlanCUs);
   const int64_t tiles = wide ? tiles64 : tiles32;
   // One row of 32-row tiles (a short prompt): every work unit would walk all
   // of K at ~0.7 us a 64-weight stage, so K splits down to one superblock per
