@@ -155,24 +155,28 @@ int run_gemm(const float* x, int64_t M, int64_t K, const qk_segment* segments, i
     const hipError_t error = hipMallocAsync(&scratch, need, stream);
     if (error != hipSuccess) return hip_fail(error, "matmul workspace allocation failed");
   }
-  hipError_t error = qk::launch_gemm_prep(x, M, K, scratch, stream);
+  // short prompt against narrow matrices: the GEMM forms its planes from x
+  bool short_form = true;
+  for (int j = 0; j < count; ++j) short_form = short_form && qk::gemm_short_plan(M, segments[j].N);
+  hipError_t error = qk::launch_gemm_prep(x, M, K, scratch, stream, short_form);
+  const float* x_short = short_form ? x : nullptr;
   // every matrix in one launch when they share its tile plan (attn q, k and v:
   // one grid of 768 tiles at M = 512 instead of 640 + 128); otherwise two of
   // one type together where they can, the rest one launch each
   bool all = false;
   if (error == hipSuccess && count > 1)
-    error = qk::launch_gemm_core_multi(scratch, segments, count, K, M, stream, all);
+    error = qk::launch_gemm_core_multi(x_short, scratch, segments, count, K, M, stream, all);
   for (int j = 0; j < count && error == hipSuccess && !all; ++j) {
     if (j + 1 < count && segments[j + 1].type == segments[j].type) {
       bool launched = false;
-      error = qk::launch_gemm_core_multi(scratch, segments + j, 2, K, M, stream, launched);
+      error = qk::launch_gemm_core_multi(x_short, scratch, segments + j, 2, K, M, stream, launched);
       if (error != hipSuccess) break;
       if (launched) {
         ++j;
         continue;
       }
     }
-    error = qk::launch_gemm_core(scratch, segments[j].w, segments[j].type, K, segments[j].N,
+    error = qk::launch_gemm_core(x_short, scratch, segments[j].w, segments[j].type, K, segments[j].N,
                                  segments[j].y, M, stream);
   }
   if (!workspace) (void)hipFreeAsync(scratch, stream);

@@ -7,35 +7,11 @@
 // [2^14, 2^15), then split into two fp16 planes hi + lo with hi = fp16(v),
 // lo = fp16(v - hi): 22 significant bits of v; and, per 32 values, 2^-5 times
 // their sum, also as hi + lo (the Q4_K min-term operand).
-#include "qk_device.hpp"
+#include "gemm_prep.hpp"
 #include "qk_launch.hpp"
 
 namespace qk {
 namespace {
-
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-
-constexpr int kHeadroomExp = 14;          // scaled magnitudes below 2^15 < fp16 max
-
-// Power-of-two exponent that brings a positive finite bound into
-// [2^14, 2^15); 0 for 0, clamped for inf/nan bounds (their products are
-// inf/nan whatever the scale).
-__device__ __forceinline__ int headroom_exponent(float bound) {
-  if (!(bound > 0.0f)) return 0;
-  if (!(bound <= 3.0e38f)) return -64;
-  return min(kHeadroomExp - ilogbf(bound), 100);  // 2^s and 2^-s stay normal floats
-}
-
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return __builtin_bit_cast(uint32_t, half2v{static_cast<_Float16>(a), static_cast<_Float16>(b)});
-}
-
-// v -> (fp16(v), fp16(v - fp16(v))) for a pair of values, packed.
-__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
-  const _Float16 ha = static_cast<_Float16>(a), hb = static_cast<_Float16>(b);
-  hi = __builtin_bit_cast(uint32_t, half2v{ha, hb});
-  lo = pack2(a - static_cast<float>(ha), b - static_cast<float>(hb));
-}
 
 // ---------------------------------------------------------------- prep ------
 
@@ -55,30 +31,9 @@ __device__ __forceinline__ void prep_group(const f32x4 a, const f32x4 b, float u
                          0, __builtin_bit_cast(int, bmax), 0xB1, 0xF, 0xF, false)));
   bmax = fmaxf(bmax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
                          0, __builtin_bit_cast(int, bmax), 0x4E, 0xF, 0xF, false)));
-  // codes round(x/amax*127) and scale amax/127 as the reference computes them
-  // in float: for amax in [2^-64, 2^64] through the exact reciprocal and
-  // Markstein quotient of the mat-vec quantiser (equal to IEEE division)
-  float code[8], scale;
-  if (bmax >= 0x1p-64f && bmax <= 0x1p64f) {
-    const float r = refined_rcp(bmax);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) code[i] = static_cast<float>(q8_code(v[i], bmax, r));
-    scale = markstein_div(bmax, 127.0f, 1.0f / 127.0f);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) code[i] = bmax == 0.0f ? 0.0f : roundf((v[i] / bmax) * 127.0f);
-    scale = bmax / 127.0f;
-  }
   uint32_t h[4], l[4];
-  float sum = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float c0 = code[2 * i], c1 = code[2 * i + 1];
-    const float s0 = (c0 * scale) * up, s1 = (c1 * scale) * up;
-    split2(s0, s1, h[i], l[i]);
-    sum += s0;
-    sum += s1;
-  }
+  float sum;
+  q8_scaled_planes(v, bmax, up, h, l, sum);
   *reinterpret_cast<u32x4*>(hi + at) = u32x4{h[0], h[1], h[2], h[3]};
   *reinterpret_cast<u32x4*>(lo + at) = u32x4{l[0], l[1], l[2], l[3]};
   sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0xB1,
@@ -195,27 +150,28 @@ size_t gemm_workspace_bytes(int64_t M, int64_t K, int type, int64_t N) {
 }
 
 hipError_t launch_gemm_prep(const float* x, int64_t M, int64_t K, void* workspace,
-                            hipStream_t stream) {
+                            hipStream_t stream, bool skip) {
+  if (skip) return hipSuccess;  // every GEMM of the call forms its planes itself
   const WorkspaceLayout ws = layout(workspace, M, K);
   prep_rows_kernel<<<static_cast<uint32_t>(M), 256, 0, stream>>>(x, ws.hi, ws.lo, ws.row_scale,
                                                                   ws.xs, static_cast<int>(K));
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_core(const void* workspace, const void* w, int type, int64_t K, int64_t N,
-                            float* y, int64_t M, hipStream_t stream) {
+hipError_t launch_gemm_core(const float* x, const void* workspace, const void* w, int type, int64_t K,
+                            int64_t N, float* y, int64_t M, hipStream_t stream) {
   const WorkspaceLayout ws = layout(const_cast<void*>(workspace), M, K);
   if (!gemm_kq_fits(M, K, N)) return hipErrorInvalidValue;
   float* partials = reinterpret_cast<float*>(static_cast<char*>(const_cast<void*>(workspace)) +
                                              partial_offset(M, K));
-  return launch_gemm_kq(type, ws.hi, ws.row_scale, ws.xs, w, K, N, y, M, partials, stream);
+  return launch_gemm_kq(type, x, ws.hi, ws.row_scale, ws.xs, w, K, N, y, M, partials, stream);
 }
 
-hipError_t launch_gemm_core_multi(const void* workspace, const qk_segment* segments, int count,
+hipError_t launch_gemm_core_multi(const float* x, const void* workspace, const qk_segment* segments, int count,
                                   int64_t K, int64_t M, hipStream_t stream, bool& launched) {
   launched = false;
   const WorkspaceLayout ws = layout(const_cast<void*>(workspace), M, K);
-  return launch_gemm_kq_multi(ws.hi, ws.row_scale, ws.xs, segments, count, K, M, stream, launched);
+  return launch_gemm_kq_multi(x, ws.hi, ws.row_scale, ws.xs, segments, count, K, M, stream, launched);
 }
 
 }  // namespace qk

@@ -49,7 +49,7 @@
 // hit 16 different bank groups.
 #include <algorithm>
 
-#include "qk_device.hpp"
+#include "gemm_prep.hpp"
 #include "qk_launch.hpp"
 
 namespace qk {
@@ -57,7 +57,6 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) uint8_t lds_byte;
 typedef __attribute__((address_space(3))) half8 lds_half8;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4_t;
@@ -77,6 +76,7 @@ struct KQCfg {
 constexpr int kKQMaxSegments = 4;
 
 struct KQGemmArgs {
+  const float* x;      // short prompts (M <= kShortM): the activations [M x K] themselves
   const _Float16* hi;  // [M x K]; lo follows at + M*K
   const _Float16* xs;  // sub-block sums: [M][S][hi 8, lo 8] (Q4_K only)
   const float* row_scale;
@@ -457,6 +457,307 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
     }
 }
 
+// ---- short prompts (M <= kShortM): one row of 32-row tiles, prep inside ----
+//
+// At M <= 32 a projection was three launches (prep, GEMM, split reduce), two of
+// them fixed cost. Here each work unit forms the planes of its own K range
+// itself, one superblock at a time, with a power-of-two scale per (row,
+// superblock): the superblock's max |x| brought into [2^14, 2^15), the Q8
+// round trip and hi/lo split of the prep kernel (gemm_prep.hpp) otherwise,
+// and 2^-s folded into the superblock's d (and dmin) instead of a row scale
+// at the end. Power-of-two scaling commutes with every rounding while no
+// value is subnormal, so the outputs are the row-scaled ones bit for bit
+// except where an fp16 plane value or the block sum of a row's far smaller
+// superblock would underflow (there this form keeps more bits). All four
+// stages of the superblock sit in LDS at once, so the stages run without
+// barriers; the next superblock's activations are in flight meanwhile.
+// Every n-tile forms the planes of its K range again, so the launch takes this
+// form only for products of at most kGemmShortTiles n-tiles (gemm_short_plan).
+// Measured at M = 23 (graph replays, against prep + GEMM (+ reduce)): attn_k
+// 11.1 -> 9.3 us, attn_v 12.7 -> 10.8, attn_q 14.3 -> 13.1, attn_output
+// 14.4 -> 13.2, ffn_down 31.2 -> 30.3; ffn_gate (76 n-tiles) 20.4 -> 21.7 and
+// the lm_head (1187) 165 -> 195, so those keep the prep launch.
+constexpr int kShortM = static_cast<int>(kGemmShortRows);
+
+struct KQShortSmem {
+  uint8_t a[4][32 * 256];  // the superblock's 4 stages: 32 rows of 8 hi + 8 lo 16-byte pieces (swizzled)
+  _Float16 xs[32][16];     // Q4_K: per row, 2^-5 x the 8 sub-block sums of v, hi then lo
+  float rs[32];            // per row: 2^-s of the superblock's scale
+};
+
+// Thread tid: row tid / 8, 32-value block tid % 8 of the superblock, whose
+// values xv holds. Writes the block's hi and lo pieces where the staging of
+// the prepared planes puts them (piece p of plane L / 8 of a stage at
+// position L ^ (row & 15), L = 8 * plane + p), its sub-block sum and the
+// row's 2^-s.
+template <int TYPE>
+__device__ __forceinline__ void short_prep(const f32x4 (&xv)[8], int tid, KQShortSmem& sm) {
+  typedef __attribute__((address_space(3))) u32x4 lds_u32x4_s;
+  const int r = tid >> 3, j = tid & 7;
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[4 * i] = xv[i].x;
+    v[4 * i + 1] = xv[i].y;
+    v[4 * i + 2] = xv[i].z;
+    v[4 * i + 3] = xv[i].w;
+  }
+  float bmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) bmax = fmaxf(bmax, fabsf(v[i]));
+  float smax = bmax;  // the row's max over the superblock: the 8 lanes of the row
+  smax = fmaxf(smax, __shfl_xor(smax, 1));
+  smax = fmaxf(smax, __shfl_xor(smax, 2));
+  smax = fmaxf(smax, __shfl_xor(smax, 4));
+  const int e = headroom_exponent(smax);
+  const float up = ldexpf(1.0f, e);
+  if (j == 0) sm.rs[r] = ldexpf(1.0f, -e);
+  // stage and first piece of the block: Q4_K stage j/2 holds blocks 2g, 2g+1
+  // (pieces 0-3, 4-7); Q6_K stage 2h + a holds groups a, a+2 of half h
+  constexpr bool kQ6 = TYPE == QK_TYPE_Q6_K;
+  const int stage = kQ6 ? 2 * (j >> 2) + (j & 1) : j >> 1;
+  const int p0 = kQ6 ? 4 * ((j >> 1) & 1) : 4 * (j & 1);
+  uint8_t* row = sm.a[stage] + r * 256;
+  float gsum[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float g[8] = {v[8 * q], v[8 * q + 1], v[8 * q + 2], v[8 * q + 3],
+                        v[8 * q + 4], v[8 * q + 5], v[8 * q + 6], v[8 * q + 7]};
+    uint32_t hh[4], ll[4];
+    q8_scaled_planes(g, bmax, up, hh, ll, gsum[q]);
+    *reinterpret_cast<lds_u32x4_s*>((__attribute__((address_space(3))) uint8_t*)(row) +
+                                    16 * ((p0 + q) ^ (r & 15))) = u32x4{hh[0], hh[1], hh[2], hh[3]};
+    *reinterpret_cast<lds_u32x4_s*>((__attribute__((address_space(3))) uint8_t*)(row) +
+                                    16 * ((8 + p0 + q) ^ (r & 15))) = u32x4{ll[0], ll[1], ll[2], ll[3]};
+  }
+  if constexpr (!kQ6) {
+    // the prep kernel's order: each lane's 8 in order, then the quad's DPP sums
+    const float t = ((gsum[0] + gsum[1]) + (gsum[2] + gsum[3])) * 0.03125f;
+    const _Float16 th = static_cast<_Float16>(t);
+    sm.xs[r][j] = th;
+    sm.xs[r][8 + j] = static_cast<_Float16>(t - static_cast<float>(th));
+  }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void kq_tile_short(const KQGemmArgs& args, KQShortSmem& sm, int nt, int split,
+                                              const uint8_t* wmat, float* ymat, int N) {
+  constexpr bool kQ6 = TYPE == QK_TYPE_Q6_K;
+  constexpr int B = kQ6 ? kQ6KBytes : kQ4KBytes;
+  constexpr int QW = kQ6 ? 2 : 1;
+  const int n0 = nt * 128;
+  const int M = args.M, K = args.K, S = args.S;
+  const int sb0 = split * S / args.splits, sb1 = (split + 1) * S / args.splits;
+  const int c_last = 4 * sb1 - 1;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+
+  // this thread's activation block of every superblock (rows past M re-read the last)
+  const float* xrow = args.x + static_cast<int64_t>(min(tid >> 3, M - 1)) * K + 32 * (tid & 7);
+  auto load_xs = [&](int sb, f32x4 (&xv)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = *reinterpret_cast<const f32x4_a4*>(xrow + 256 * sb + 4 * i);
+  };
+  const uint8_t* wrow = wmat + static_cast<int64_t>(min(n0 + wave * 32 + l32, N - 1)) * S * B;
+  auto load_head = [&](int sb, u32x4& hd, uint32_t& dd) {
+    const uint8_t* p = wrow + sb * B;
+    if constexpr (kQ6) {
+      hd = load16_a2(p + 192);
+      dd = load_u16(p + 208);
+    } else {
+      hd = load16(p);
+      dd = 0;
+    }
+  };
+  auto load_q = [&](int c, u32x4 (&q)[QW]) {
+    const int g = c & 3;
+    const uint8_t* p = wrow + (c >> 2) * B;
+    if constexpr (kQ6) {
+      q[0] = load16_a2(p + 64 * (g >> 1) + 32 * (g & 1) + 16 * h);
+      q[1] = load16_a2(p + 128 + 32 * (g >> 1) + 16 * h);
+    } else {
+      q[0] = load16(p + 16 + 32 * g + 16 * h);
+    }
+  };
+
+  f32x16 acc, ph;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = ph[r] = 0.0f;
+  u32x4 wh[2], bq[2][QW];
+  uint32_t wd[2];
+  f32x4 xv[8];
+  load_xs(sb0, xv);
+  load_head(sb0, wh[0], wd[0]);
+  load_q(4 * sb0, bq[0]);
+
+  typedef __attribute__((address_space(3))) uint8_t lds_b;
+  typedef __attribute__((address_space(3))) half8 lds_h8;
+  typedef __attribute__((address_space(3))) f32x4 lds_f4;
+  const int swz = l32 & 15;
+  auto superblock = [&](int sb, const u32x4& hcur, uint32_t dcur, u32x4& hnext, uint32_t& dnext) {
+    __syncthreads();  // every wave is past the previous superblock's stages and fold
+    short_prep<TYPE>(xv, tid, sm);
+    load_xs(min(sb + 1, sb1 - 1), xv);  // the next superblock's, in flight during the stages
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c = 4 * sb + g;
+      load_q(min(c + 1, c_last), bq[(g + 1) & 1]);
+      if (g == 2) load_head(min(sb + 1, sb1 - 1), hnext, dnext);
+      __builtin_amdgcn_sched_barrier(0);
+      half2v cm[2], ce[2];
+      if constexpr (kQ6) {
+#pragma unroll
+        for (int U = 0; U < 2; ++U) {
+          const int scv = __builtin_amdgcn_sbfe(static_cast<int>(hcur[2 * (g >> 1) + U]), 8 * (2 * (g & 1)) + 8 * h, 8);
+          const _Float16 sh = static_cast<_Float16>(static_cast<int16_t>(scv));
+          cm[U] = half2v{sh, sh};
+        }
+      } else {
+        int sc0, mn0, sc1, mn1;
+        scale_min_k4(2 * g, hcur.y, hcur.z, hcur.w, sc0, mn0);
+        scale_min_k4(2 * g + 1, hcur.y, hcur.z, hcur.w, sc1, mn1);
+        const _Float16 s0 = static_cast<_Float16>(static_cast<uint16_t>(sc0));
+        const _Float16 s1 = static_cast<_Float16>(static_cast<uint16_t>(sc1));
+        cm[0] = half2v{s0, s0};
+        ce[0] = cm[0] * half2v{-1024.0f16, -1024.0f16};
+        const half2v t1{s1, s1};
+        cm[1] = t1 * half2v{0.0625f16, 0.0625f16};
+        ce[1] = t1 * half2v{-64.0f16, -64.0f16};
+        (void)mn0;
+        (void)mn1;
+      }
+      const lds_b* a_row = (const lds_b*)(sm.a[g]) + l32 * 256;
+      auto read_a = [&](int step, half8& ah, half8& al) {
+        const int p = 4 * (step >> 1) + 2 * h + (step & 1);
+        ah = *reinterpret_cast<const lds_h8*>(a_row + 16 * (p ^ swz));
+        al = *reinterpret_cast<const lds_h8*>(a_row + 16 * ((8 + p) ^ swz));
+      };
+      auto convert = [&](int step, half8& bw, half8& bx) {
+        const int U = step >> 1, s2 = step & 1;
+        const u32x4 q = bq[g & 1][0];
+        if constexpr (kQ6) {
+          const u32x4 qh = bq[g & 1][QW - 1];
+          if (U)
+            weights_q6k<1>(q[2 * s2], q[2 * s2 + 1], qh[2 * s2], qh[2 * s2 + 1], 2 * (g & 1) + 4, cm[1], bw, bx);
+          else
+            weights_q6k<0>(q[2 * s2], q[2 * s2 + 1], qh[2 * s2], qh[2 * s2 + 1], 2 * (g & 1), cm[0], bw, bx);
+        } else {
+          bw = U ? weights_fp16<1>(q[2 * s2], q[2 * s2 + 1], cm[1], ce[1])
+                 : weights_fp16<0>(q[2 * s2], q[2 * s2 + 1], cm[0], ce[0]);
+          bx = bw;
+        }
+      };
+      half8 ah[2], al[2], bw[2], bx[2];
+      read_a(0, ah[0], al[0]);
+      read_a(1, ah[1], al[1]);
+      convert(0, bw[0], bx[0]);
+#pragma unroll
+      for (int step = 0; step < 4; ++step) {
+        const int ab = step & 1;
+        ph = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[ab], bw[ab], ph, 0, 0, 0);
+        ph = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[ab], bw[ab], ph, 0, 0, 0);
+        if constexpr (kQ6) ph = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[ab], bx[ab], ph, 0, 0, 0);
+        if (step < 3) convert(step + 1, bw[(step + 1) & 1], bx[(step + 1) & 1]);
+        if (step + 2 < 4) read_a(step + 2, ah[ab], al[ab]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // superblock end: acc += (d 2^-s(m)) * part (Q4_K: - (32 dmin 2^-s(m)) * (X . m))
+    float rsr[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 t = *reinterpret_cast<const lds_f4*>((const lds_b*)(sm.rs) + 4 * (8 * i + 4 * h));
+      rsr[4 * i] = t.x;
+      rsr[4 * i + 1] = t.y;
+      rsr[4 * i + 2] = t.z;
+      rsr[4 * i + 3] = t.w;
+    }
+    if constexpr (kQ6) {
+      const float d = half_bits_to_float(dcur);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[r] = fmaf(d * rsr[r], ph[r], acc[r]);
+        ph[r] = 0.0f;
+      }
+    } else {
+      const float dd = half_bits_to_float(hcur.x & 0xFFFFu);
+      const float dm = -32.0f * half_bits_to_float(hcur.x >> 16);
+      u32x4 min_b;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int sa, ma, sb2, mb;
+        scale_min_k4(2 * q, hcur.y, hcur.z, hcur.w, sa, ma);
+        scale_min_k4(2 * q + 1, hcur.y, hcur.z, hcur.w, sb2, mb);
+        const half2v mm{static_cast<_Float16>(static_cast<uint16_t>(ma)), static_cast<_Float16>(static_cast<uint16_t>(mb))};
+        min_b[q] = __builtin_bit_cast(uint32_t, mm);
+      }
+      const u32x4 xa = *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+          (const lds_b*)(&sm.xs[0][0]) + 32 * l32 + 16 * h);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = fmaf(dd * rsr[r], ph[r], acc[r]);
+      f32x16 zero;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
+      ph = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, xa), __builtin_bit_cast(half8, min_b), zero,
+                                                  0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[r] = fmaf(dm * rsr[r], ph[r], acc[r]);
+        ph[r] = 0.0f;
+      }
+    }
+  };
+  for (int sb = sb0; sb < sb1; sb += 2) {
+    superblock(sb, wh[0], wd[0], wh[1], wd[1]);
+    if (sb + 1 < sb1) superblock(sb + 1, wh[1], wd[1], wh[0], wd[0]);
+  }
+
+  // epilogue: y (the scales are in acc already), or the partial of this split
+  float* const part = args.part + static_cast<int64_t>(split) * M * N;
+  const int n = n0 + wave * 32 + l32;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = 8 * (r >> 2) + 4 * h + (r & 3);
+    if (m >= M || n >= N) continue;
+    if (args.splits == 1)
+      ymat[static_cast<int64_t>(m) * N + n] = acc[r];
+    else
+      part[static_cast<int64_t>(m) * N + n] = acc[r];
+  }
+}
+
+// The short-prompt GEMM: grid, work units and matrices as gemm_kq_kernel's
+// (one row of 32 x 128 tiles).
+template <int TYPE>
+__global__ __launch_bounds__(64 * kWaves, 3) void gemm_kq_short_kernel(const KQGemmArgs args) {
+  __shared__ __align__(16) KQShortSmem sm;
+  const int b = static_cast<int>(blockIdx.x);
+  const int u = (b & 7) * args.per_xcd + (b >> 3);
+  if ((b >> 3) >= args.per_xcd || u >= args.tiles * args.splits) return;
+  const int nt = u / args.splits, split = u % args.splits;
+  const int nseg = args.nseg;
+  const int j = (nseg > 1 && nt >= args.tile0[1]) + (nseg > 2 && nt >= args.tile0[2]) +
+                (nseg > 3 && nt >= args.tile0[3]);
+  auto pick = [j](auto f0, auto f1, auto f2, auto f3) {
+    return j == 0 ? f0 : j == 1 ? f1 : j == 2 ? f2 : f3;
+  };
+  const uint8_t* wmat = pick(args.w[0], args.w[1], args.w[2], args.w[3]);
+  float* ymat = pick(args.y[0], args.y[1], args.y[2], args.y[3]);
+  const int N = pick(args.N[0], args.N[1], args.N[2], args.N[3]);
+  const int nt_local = nt - pick(args.tile0[0], args.tile0[1], args.tile0[2], args.tile0[3]);
+  if constexpr (TYPE != 0) {
+    kq_tile_short<TYPE>(args, sm, nt_local, split, wmat, ymat, N);
+  } else {
+    if (pick(args.type[0], args.type[1], args.type[2], args.type[3]) == QK_TYPE_Q4_K)
+      kq_tile_short<QK_TYPE_Q4_K>(args, sm, nt_local, split, wmat, ymat, N);
+    else
+      kq_tile_short<QK_TYPE_Q6_K>(args, sm, nt_local, split, wmat, ymat, N);
+  }
+}
+
 // TYPE: the weight type of every matrix of the launch, or 0 for matrices of
 // both types (each workgroup takes its matrix's). Register budget: three
 // workgroups per CU (168 VGPRs) except the Q6_K kernels, whose 64-row tile
@@ -501,7 +802,8 @@ __global__ __launch_bounds__(64 * kWaves, TYPE == QK_TYPE_Q6_K ? 2 : 3) void gem
   }
 }
 
-// y[m][n] = (partial 0 + partial 1 + ...) * 2^-s(m), the splits added in
+// y[m][n] = (partial 0 + partial 1 + ...) * 2^-s(m) (row_scale null: the
+// short-prompt GEMM's partials carry their scales), the splits added in
 // order (results do not depend on timing). Grid (ceil(N / 256), M). The
 // partials were written on every XCD and miss this one's L2, so each thread
 // has 16 splits' loads in flight at once (indices past the last re-read it)
@@ -524,7 +826,7 @@ __global__ __launch_bounds__(256) void gemm_kq_reduce_kernel(const float* __rest
     for (int kk = 0; kk < kBatch; ++kk)
       if (k0 + kk < splits) v = k0 + kk == 0 ? p[kk] : v + p[kk];
   }
-  y[at] = v * row_scale[m];
+  y[at] = row_scale ? v * row_scale[m] : v;
 }
 
 template <int TYPE, int TM, int TN>
@@ -540,6 +842,21 @@ hipError_t launch_cfg(KQGemmArgs a, hipStream_t stream) {
   note("gemm_kq_kernel", 8 * a.per_xcd, TYPE, TM, TN, a.splits);
   hipLaunchKernelGGL((gemm_kq_kernel<TYPE, TM, TN>), dim3(static_cast<uint32_t>(8 * a.per_xcd)),
                      dim3(64 * kWaves), 0, stream, a);
+  return hipGetLastError();
+}
+
+template <int TYPE>
+hipError_t launch_short(KQGemmArgs a, hipStream_t stream) {
+  a.n_tiles = 0;
+  for (int j = 0; j < a.nseg; ++j) {
+    a.tile0[j] = a.n_tiles;
+    a.n_tiles += (a.N[j] + 127) / 128;
+  }
+  a.tiles = a.n_tiles;  // one row of tiles
+  a.per_xcd = (a.tiles * a.splits + 7) / 8;
+  note("gemm_kq_short_kernel", 8 * a.per_xcd, TYPE, a.splits);
+  hipLaunchKernelGGL((gemm_kq_short_kernel<TYPE>), dim3(static_cast<uint32_t>(8 * a.per_xcd)), dim3(64 * kWaves), 0,
+                     stream, a);
   return hipGetLastError();
 }
 
@@ -600,11 +917,14 @@ size_t gemm_kq_partial_bytes(int type, int64_t M, int64_t K, int64_t N) {
   return p.splits > 1 ? static_cast<size_t>(p.splits) * M * N * sizeof(float) : 0;
 }
 
-hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, const void* xsums,
-                          const void* w, int64_t K, int64_t N, float* y, int64_t M, float* partials,
-                          hipStream_t stream) {
+hipError_t launch_gemm_kq(int type, const float* x, const _Float16* hi, const float* row_scale,
+                          const void* xsums, const void* w, int64_t K, int64_t N, float* y, int64_t M,
+                          float* partials, hipStream_t stream) {
   const KQPlan p = plan(type, M, N, K);
+  const bool short_m = x != nullptr;  // the short form: planes formed from x in the GEMM
+  if (short_m && M > kShortM) return hipErrorInvalidValue;
   KQGemmArgs a{};
+  a.x = x;
   a.hi = hi;
   a.xs = static_cast<const _Float16*>(xsums);
   a.row_scale = row_scale;
@@ -620,18 +940,20 @@ hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, 
   a.splits = p.splits;
   if (p.splits > 1 && partials == nullptr) return hipErrorInvalidValue;
   hipError_t e;
-  if (type == QK_TYPE_Q6_K)
+  if (short_m)
+    e = type == QK_TYPE_Q6_K ? launch_short<QK_TYPE_Q6_K>(a, stream) : launch_short<QK_TYPE_Q4_K>(a, stream);
+  else if (type == QK_TYPE_Q6_K)
     e = p.wide ? launch_cfg<QK_TYPE_Q6_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q6_K, 1, 1>(a, stream);
   else
     e = p.wide ? launch_cfg<QK_TYPE_Q4_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q4_K, 1, 1>(a, stream);
   if (e != hipSuccess || p.splits == 1) return e;
   gemm_kq_reduce_kernel<<<dim3(static_cast<uint32_t>((N + 255) / 256), static_cast<uint32_t>(M)), 256,
-                          0, stream>>>(partials, row_scale, y, static_cast<int>(M),
+                          0, stream>>>(partials, short_m ? nullptr : row_scale, y, static_cast<int>(M),
                                        static_cast<int>(N), p.splits);
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, const void* xsums,
+hipError_t launch_gemm_kq_multi(const float* x, const _Float16* hi, const float* row_scale, const void* xsums,
                                 const qk_segment* segments, int count, int64_t K, int64_t M,
                                 hipStream_t stream, bool& launched) {
   launched = false;
@@ -659,13 +981,16 @@ hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, cons
   // The tile shape of the combined grid. The mixed-type kernel exists for
   // 32 x 128 tiles only: it is taken while the grid has fewer than two
   // 64 x 128 tiles per CU (q + k + v at M = 512: 384), else same-type pairs run.
+  const bool short_m = x != nullptr;
+  if (short_m && M > kShortM) return hipErrorInvalidValue;
   bool wide = false;
-  if (type == 0) {
+  if (type == 0 && !short_m) {
     if (((M + 63) / 64) * ((total + 127) / 128) >= 2 * kPlanCUs) return hipSuccess;
-  } else {
+  } else if (type != 0) {
     wide = plan(type, M, total, K).wide;
   }
   KQGemmArgs a{};
+  a.x = x;
   a.hi = hi;
   a.xs = static_cast<const _Float16*>(xsums);
   a.row_scale = row_scale;
@@ -682,7 +1007,10 @@ hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, cons
   a.S = static_cast<int32_t>(K / 256);
   a.splits = 1;
   hipError_t e;
-  if (type == 0)
+  if (short_m)
+    e = type == 0 ? launch_short<0>(a, stream)
+                  : type == QK_TYPE_Q6_K ? launch_short<QK_TYPE_Q6_K>(a, stream) : launch_short<QK_TYPE_Q4_K>(a, stream);
+  else if (type == 0)
     e = launch_cfg<0, 1, 1>(a, stream);
   else if (type == QK_TYPE_Q6_K)
     e = wide ? launch_cfg<QK_TYPE_Q6_K, 2, 1>(a, stream) : launch_cfg<QK_TYPE_Q6_K, 1, 1>(a, stream);

@@ -123,14 +123,27 @@ constexpr int64_t kGemvMaxRows = 8;
 // the partial products of an N-column product of this type; rounded up to 256.
 size_t gemm_workspace_bytes(int64_t M, int64_t K, int type, int64_t N);
 
-// workspace (>= gemm_workspace_bytes(M, K, ...), 16-byte aligned) = fp16 of
-// the Q8 round trip of x[M x K], row scales, block sums.
-hipError_t launch_gemm_prep(const float* x, int64_t M, int64_t K, void* workspace,
-                            hipStream_t stream);
+// A short prompt (at most kGemmShortRows rows) times matrices of at most
+// kGemmShortTiles 128-column tiles each: the GEMM forms its activation planes
+// itself (no prep launch). A call's matrices either all take this form or all
+// take the prep (the GEMM launches below get x, or null and the prepared
+// workspace).
+constexpr int64_t kGemmShortRows = 32;
+constexpr int64_t kGemmShortTiles = 32;
+inline bool gemm_short_plan(int64_t M, int64_t N) {
+  return M <= kGemmShortRows && (N + 127) / 128 <= kGemmShortTiles;
+}
 
-// y[M x N] = workspace . dequant(W)^T on MFMA, fp32 accumulation.
-hipError_t launch_gemm_core(const void* workspace, const void* w, int type, int64_t K, int64_t N,
-                            float* y, int64_t M, hipStream_t stream);
+// workspace (>= gemm_workspace_bytes(M, K, ...), 16-byte aligned) = fp16 of
+// the Q8 round trip of x[M x K], row scales, block sums (not needed when every
+// product of the call takes the short form: `skip`).
+hipError_t launch_gemm_prep(const float* x, int64_t M, int64_t K, void* workspace,
+                            hipStream_t stream, bool skip = false);
+
+// y[M x N] = x . dequant(W)^T on MFMA, fp32 accumulation, over the prepared
+// workspace (M <= kGemmShortRows: over x itself).
+hipError_t launch_gemm_core(const float* x, const void* workspace, const void* w, int type, int64_t K,
+                            int64_t N, float* y, int64_t M, hipStream_t stream);
 
 // The Q4_K / Q6_K GEMM (gemm_kquant.hip) over the prepared planes: hi (lo
 // follows it), row scales and (Q4_K) sub-block sums of the workspace, partial
@@ -138,19 +151,19 @@ hipError_t launch_gemm_core(const void* workspace, const void* w, int type, int6
 // gemm_kq_fits: the shape is within its 32-bit tile and row indices.
 bool gemm_kq_fits(int64_t M, int64_t K, int64_t N);
 size_t gemm_kq_partial_bytes(int type, int64_t M, int64_t K, int64_t N);
-hipError_t launch_gemm_kq(int type, const _Float16* hi, const float* row_scale, const void* xsums,
-                          const void* w, int64_t K, int64_t N, float* y, int64_t M, float* partials,
-                          hipStream_t stream);
+hipError_t launch_gemm_kq(int type, const float* x, const _Float16* hi, const float* row_scale,
+                          const void* xsums, const void* w, int64_t K, int64_t N, float* y, int64_t M,
+                          float* partials, hipStream_t stream);
 
 // 2..4 weight matrices of width K (either type) on the same prepared
 // activations in one launch (attn q, k and v; gate and up): launched (and
 // `launched` set) when none needs a split K and all take the combined grid's
 // tile shape, else nothing is enqueued. Each output equals its single launch's
 // bit for bit.
-hipError_t launch_gemm_kq_multi(const _Float16* hi, const float* row_scale, const void* xsums,
+hipError_t launch_gemm_kq_multi(const float* x, const _Float16* hi, const float* row_scale, const void* xsums,
                                 const qk_segment* segments, int count, int64_t K, int64_t M,
                                 hipStream_t stream, bool& launched);
-hipError_t launch_gemm_core_multi(const void* workspace, const qk_segment* segments, int count,
+hipError_t launch_gemm_core_multi(const float* x, const void* workspace, const qk_segment* segments, int count,
                                   int64_t K, int64_t M, hipStream_t stream, bool& launched);
 
 // Bytes of the argmax workspace (zero-filled once by the caller).

@@ -225,6 +225,42 @@ def test_gemm_model_matches_oracle(oracle, qtype, TM, TN, K, splits):
     assert err <= 1e-6
 
 
+@pytest.mark.parametrize("q6", [False, True])
+def test_short_prompt_prep_writes_the_staged_slot_images(q6):
+    """At M <= 32 the GEMM forms a superblock's four stages in LDS itself
+    (thread t: row t // 8, the 32-value block t % 8 of the superblock, 4
+    pieces of 8 values per plane). Every (stage, row, 16-byte position) of the
+    four slots is written exactly once, with the plane and the k range that
+    the staging of prepared planes (thread f: row f // 16, position f % 16,
+    piece (f % 16) ^ (row % 16)) puts there; the sub-block sums land where a
+    lane (row l32, half h) reads its 16 bytes."""
+    expect = {}
+    for g in range(4):
+        for r in range(32):
+            for pos in range(16):
+                L = pos ^ (r & 15)
+                plane, p = L >> 3, L & 7
+                k0 = stage_k(q6, g) + (64 * (p >> 2) + 8 * (p & 3) if q6 else 8 * p)
+                expect[(g, r, pos)] = (plane, k0)
+    got, xs = {}, {}
+    for t in range(256):
+        r, j = t >> 3, t & 7
+        stage = 2 * (j >> 2) + (j & 1) if q6 else j >> 1
+        p0 = 4 * ((j >> 1) & 1) if q6 else 4 * (j & 1)
+        for q in range(4):
+            for plane in range(2):
+                key = (stage, r, (8 * plane + p0 + q) ^ (r & 15))
+                assert key not in got
+                got[key] = (plane, 32 * j + 8 * q)
+        xs[2 * (16 * r + j)] = ("hi", r, j)       # byte offsets in the 32 x 16 halves
+        xs[2 * (16 * r + 8 + j)] = ("lo", r, j)
+    assert got == expect
+    for l32 in range(32):
+        for h in range(2):
+            for i in range(8):
+                assert xs[32 * l32 + 16 * h + 2 * i] == (("hi", "lo")[h], l32, i)
+
+
 def test_a_slot_swizzle_is_conflict_free():
     """The 16 rows one ds_read_b128 pass serves (lanes 16k .. 16k+15 of a half-wave)
     read 16 different 16-byte positions of their 256-byte rows, for every piece."""

@@ -170,6 +170,48 @@ def test_prefill_ragged_against_oracle(gpu, oracle, qtype, M, N, K):
 
 
 @pytest.mark.parametrize("qtype", [Q4, Q6])
+@pytest.mark.parametrize("M,N,K,scale", [(23, 200, 2560, 1.0), (32, 128, 768, 1e-6), (9, 300, 256, 1e4),
+                                         (31, 1000, 4096, 1.0), (17, 2560, 9728, 1.0)])
+def test_prefill_short_prompt_against_oracle(gpu, oracle, qtype, M, N, K, scale):
+    """M <= 32 (a short prompt): the GEMM forms its own activation planes, with
+    a power-of-two scale per row and superblock, in one launch (plus the split
+    reduce). Ragged N, one to 38 superblocks, activations scaled by 1e-6 and
+    1e4, against the oracle's double-accumulated product."""
+    print(f"[case] short type={qtype} M={M} N={N} K={K} x*{scale:g}", flush=True)
+    w = make_weight(gpu, qtype, N, K, SEED + 70 + M + N)
+    x = (oracle.synth_normal(M * K, SEED + 71 + K) * np.float32(scale)).astype(np.float32)
+    xd = gpu.DeviceBuffer.from_array(x)
+    y = gpu.DeviceBuffer(4 * M * N)
+    gpu.matmul(xd, w, qtype, K, N, y, M)
+    gpu.synchronize()
+    print(f"[case] launch {gpu.last_launch()}", flush=True)
+    got = y.download(np.float32).reshape(M, N)
+    ref = oracle.reference_product(x, w.download(np.uint8), qtype, K, N)
+    check(oracle, got, ref.reshape(M, N), f"short {qtype} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6])
+def test_prefill_short_prompt_superblocks_of_unequal_size(gpu, oracle, qtype):
+    """Rows whose superblocks differ by up to 10^7 in magnitude: each
+    superblock gets its own power-of-two scale, so the small ones keep their
+    precision (checked element by element: the reference's Approx on >= 99%
+    of the elements and, per row, the error of every output within 1e-5 of the
+    row norm)."""
+    M, N, K = 23, 320, 2560
+    w = make_weight(gpu, qtype, N, K, SEED + 80)
+    x = oracle.synth_normal(M * K, SEED + 81).reshape(M, K // 256, 256)
+    mags = np.float32(10.0) ** np.arange(-3, 7, dtype=np.float32)[: K // 256]
+    x = (x * mags[None, :, None]).astype(np.float32).reshape(-1)
+    xd = gpu.DeviceBuffer.from_array(x)
+    y = gpu.DeviceBuffer(4 * M * N)
+    gpu.matmul(xd, w, qtype, K, N, y, M)
+    gpu.synchronize()
+    got = y.download(np.float32).reshape(M, N)
+    ref = oracle.reference_product(x, w.download(np.uint8), qtype, K, N).reshape(M, N)
+    check(oracle, got, ref, f"unequal superblocks {qtype}")
+
+
+@pytest.mark.parametrize("qtype", [Q4, Q6])
 def test_prefill_zero_input_and_reuse(gpu, oracle, qtype):
     """src/tests/MatmulTests.cpp:12-82 and :84-132 at M > 8: zero rows give exact zeros,
     a reused output is overwritten, two streams give identical bits."""
@@ -251,6 +293,8 @@ def test_prefill_entry_points_agree_bitwise(gpu, oracle, qtype):
     (77, 2560, [(Q6, 333), (Q6, 129), (Q4, 200), (Q4, 64)]),
     (40, 2560, [(Q4, 4096), (Q4, 1024), (Q6, 1024)]),
     (64, 9728, [(Q6, 256), (Q4, 300)]),                    # split K: separate launches
+    (20, 256, [(Q6, 300), (Q4, 200), (Q4, 64)]),            # short prompt, one launch of both types
+    (23, 2560, [(Q4, 4096), (Q4, 1024), (Q6, 1024)]),       # short prompt, split K: separate launches
 ])
 def test_prefill_segments_pairs_match_single_launches(gpu, oracle, M, K, shapes):
     """qk_matmul_segments at M > 8 runs its matrices in one GEMM launch when
