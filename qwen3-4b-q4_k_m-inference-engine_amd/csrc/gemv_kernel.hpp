@@ -422,13 +422,21 @@ __device__ __forceinline__ uint64_t matvec_body(const MatvecArgs& a, int row_lo,
         // became v_mad_u64_u32 with an unrelated register as its high half,
         // and a wait for that register's pending weight load.
         const int blk = (min(s_raw, S - 1) * 8 + blk_a) & 0xFFFF;
+        // A Q6_K piece is unpacked once for all MT rows, and the rows' LDS
+        // reads go out two rows at a time (hoisted all at once, with the
+        // codes recomputed per row, 10-14 VGPRs spilled at MT = 8).
+        [[maybe_unused]] Q6KCodes cd;
+        if constexpr (TYPE != QK_TYPE_Q4_K) cd = unpack_q6k_piece(f[i], pc);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           const lds_q8_block* xr = xq + m * S * 8 + blk;
-          const float v = dot_piece<TYPE>(f[i], load_x(xr), load_x(xr + blk_step), pc, TYPE);
+          float v;
+          if constexpr (TYPE == QK_TYPE_Q4_K) v = dot_q4k_piece(f[i], load_x(xr), load_x(xr + blk_step), pc);
+          else v = dot_q6k_codes(cd, load_x(xr), load_x(xr + blk_step));
           const float add = s_raw < S ? v : 0.0f;
           if (phase) up[m] += add;
           else acc[m] += add;
+          if (MT > 1 && (m & 1)) __builtin_amdgcn_sched_barrier(0);
         }
         if (cc.k == ipu_total - 1) {  // the group's last iteration: reduce and store
           const int row = group_row(cc.u) + rr;
