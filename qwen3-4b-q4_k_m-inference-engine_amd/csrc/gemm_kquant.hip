@@ -436,18 +436,23 @@ __device__ __forceinline__ void kq_tile(const KQGemmArgs& args, uint8_t (&slots)
     if (sb + 1 < sb1) superblock(sb + 1, wh[1], wd[1], wh[0], wd[0]);
   }
 
-  // epilogue: y = acc * 2^-s(m), or the unscaled partial of this split
+  // epilogue: y = acc * 2^-s(m), or the unscaled partial of this split. The
+  // lane's half and column come from the lane id again here (mbcnt), so no
+  // register is held across the superblock loop for them (the 64-row Q4_K
+  // tile spilled three there).
+  const int el = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+  const int eh = el >> 5, el32 = el & 31;
   float* const part = args.part + static_cast<int64_t>(split) * M * N;
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+      const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * eh + (r & 3);
       if (m >= M) continue;
       const float rs = args.row_scale[m];
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wave * 32 * TN + 32 * j + l32;
+        const int n = n0 + wave * 32 * TN + 32 * j + el32;
         if (n >= N) continue;
         if (args.splits == 1)
           ymat[static_cast<int64_t>(m) * N + n] = acc[i][j][r] * rs;
