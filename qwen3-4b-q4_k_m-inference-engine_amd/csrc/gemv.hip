@@ -105,6 +105,9 @@ hipError_t launch_matvec(MatvecParams p, int mode, hipStream_t stream) {
   if (e != hipSuccess || launched) return e;
   e = launch_bmv(p, mode, stream, launched);
   if (e != hipSuccess || launched) return e;
+  // very tall matrices (the lm_head) at M = 2..8: the multi-pass batched form
+  e = launch_bmv_pass(p, mode, stream, launched);
+  if (e != hipSuccess || launched) return e;
   // Shapes whose per-CU share fits in LDS take the whole-share kernel
   // (gemv_stream.hip).
   e = launch_stream_matvec(p, mode, stream, launched);

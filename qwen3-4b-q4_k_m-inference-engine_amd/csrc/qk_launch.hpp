@@ -81,6 +81,14 @@ hipError_t launch_bmv_ws(const MatvecParams& p, int mode, hipStream_t stream, bo
 // shape fits its LDS plan.
 hipError_t launch_bmv(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
 
+// The multi-pass batched mat-vec on the int8 matrix cores (bmv_pass.hip): M =
+// 2..8 rows of fp32 activations, mode 0, one matrix tall enough for two
+// 16-row groups per wave (the lm_head); launched (and `launched` set) when it
+// takes the shape. bmv_pass_plan: superblock columns per pass, 16-byte chunks
+// per run and per lane (false when a one-column pass needs more than 8 KB).
+hipError_t launch_bmv_pass(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
+bool bmv_pass_plan(int64_t S, int type, int& C, int& cpr, int& J);
+
 // Compute units and LDS bytes per workgroup of the current device (cached).
 hipError_t device_limits(int& cus, int& max_lds);
 // Sets a kernel's dynamic LDS limit to `lds` bytes (once per kernel and size).

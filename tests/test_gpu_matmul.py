@@ -241,6 +241,23 @@ def test_matmul_batched_qwen3_shapes(gpu, oracle, name, M):
     assert_parity(oracle, got, ref)
 
 
+@pytest.mark.parametrize("qtype,K,N,M", [(Q4, 768, 70001, 3), (Q4, 2560, 66000, 8), (Q6, 2816, 65600, 2),
+                                         (Q6, 768, 70003, 7), (Q6, 256, 66000, 5)])
+def test_matmul_batched_tall_matrices(gpu, oracle, qtype, K, N, M):
+    """M = 2..8 against matrices tall enough for two 16-row groups per wave
+    (the lm_head's kind) take the multi-pass batched kernel: passes of 16 rows
+    x C superblock columns through each wave's LDS slot. Ragged last groups (N
+    not a multiple of 16), Q6_K rows of an odd superblock count (2-byte
+    aligned runs), a pass shorter than C at the row end, one-superblock rows."""
+    w = make_weight(gpu, oracle, qtype, N, K, SEED + 700 + N + K)
+    x = oracle.synth_normal(M * K, SEED + 41 + M)
+    got = run_matmul(gpu, w, qtype, K, N, x, M)
+    print(f"[case] tall type={qtype} K={K} N={N} M={M} launch {gpu.last_launch()}", flush=True)
+    assert gpu.last_launch().startswith("bmv_pass_kernel")
+    ref = oracle.reference_product(x, w.download(np.uint8), qtype, K, N)
+    assert_parity(oracle, got, ref)
+
+
 @pytest.mark.parametrize("qtype,K", [(Q4, 2560), (Q6, 2560), (Q4, 4096), (Q6, 9728)])
 @pytest.mark.parametrize("rows", [1, 4, 5, 101])
 def test_matmul_rows_truncated_columns(gpu, oracle, qtype, K, rows):
