@@ -183,7 +183,8 @@ int qk_ffn_gate_up_norm(const float *x, const float *norm, float eps, const void
                         qk_stream_t stream);
 
 /* Bytes of the workspace qk_ffn needs: its grid-barrier words, then room for
- * Q8(h) (160 KiB) and the RMSNorm rows (512 KiB) of the batched M = 2..8 block.
+ * Q8(h) (160 KiB), the RMSNorm rows (512 KiB) and the Q8(h) block arrival
+ * counters (8 KiB) of the batched M = 2..8 block.
  * The caller zero-fills it once before its first use; every call leaves it
  * ready for the next. Calls that may run concurrently need separate
  * workspaces. */
@@ -206,8 +207,10 @@ size_t qk_ffn_workspace_size(void);
  * checks after each replay of a step, or at least before it trusts a token).
  * M = 2..8 (when M*N/32 Q8 blocks fit in
  * 160 KiB, M*K norm rows in 512 KiB and M rows of Q8(h) in one down launch):
- * the norm into the workspace, qk_ffn_gate_up, h quantised once into the
- * workspace, then the down mat-vec on those Q8 blocks; nothing is allocated.
+ * the norm into the workspace, qk_ffn_gate_up with h quantised once into the
+ * workspace (in the gate/up launch, by the workgroup that completes each
+ * 32-value block, when N/32 counters fit in 8 KiB; else by a launch of its
+ * own), then the down mat-vec on those Q8 blocks; nothing is allocated.
  * Other M or shapes: qk_ffn_gate_up(_norm) then qk_matmul on the stream
  * (allocating at M > 8 as they do). Validation
  * as qk_matmul for both weights, plus the workspace (256-byte aligned, at

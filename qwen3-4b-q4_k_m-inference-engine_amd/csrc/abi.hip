@@ -458,8 +458,11 @@ int qk_ffn_gate_up_norm(const float* x, const float* norm, float eps, const void
 // instead of in every CU of the down launch.
 constexpr size_t kFfnQ8Bytes = size_t{160} << 10;    // Q8 image of h, M*N/32 blocks
 constexpr size_t kFfnNormBytes = size_t{512} << 10;  // RMSNorm(x) rows, M*K floats
+constexpr size_t kFfnArriveBytes = size_t{8} << 10;  // Q8(h) block arrival counters, N/32 words
 
-size_t qk_ffn_workspace_size(void) { return qk::ffn_sync_bytes() + kFfnQ8Bytes + kFfnNormBytes; }
+size_t qk_ffn_workspace_size(void) {
+  return qk::ffn_sync_bytes() + kFfnQ8Bytes + kFfnNormBytes + kFfnArriveBytes;
+}
 
 int qk_ffn(const float* x, const float* norm, float eps, const void* gate, const void* up,
            int gate_up_type, const void* down, int down_type, int64_t K, int64_t N, float* h, float* y,
@@ -492,7 +495,9 @@ int qk_ffn(const float* x, const float* norm, float eps, const void* gate, const
     if (launched) return QK_OK;
   }
   // M = 2..8 with a full workspace: RMSNorm rows and Q8(h) in the workspace;
-  // gate/up, one quantisation of h, the down mat-vec on the Q8 blocks.
+  // gate/up with h quantised once (in the gate/up launch when the batched
+  // kernel takes it, else by its own launch), the down mat-vec on the Q8
+  // blocks.
   const size_t q8_bytes = static_cast<size_t>(M) * static_cast<size_t>(N / 32) * sizeof(qk_q8_block);
   const size_t norm_bytes = norm ? static_cast<size_t>(M * K) * sizeof(float) : 0;
   if (M >= 2 && M <= 8 && q8_bytes <= kFfnQ8Bytes && norm_bytes <= kFfnNormBytes &&
@@ -506,10 +511,27 @@ int qk_ffn(const float* x, const float* norm, float eps, const void* gate, const
       if (error != hipSuccess) return hip_fail(error, "RMSNorm launch failed");
       xin = normalized;
     }
-    status = qk_ffn_gate_up(xin, gate, up, gate_up_type, K, N, h, M, stream);
-    if (status != QK_OK) return status;
-    const hipError_t error = qk::launch_quantize_q8(h, M, N, hq, s);
-    if (error != hipSuccess) return hip_fail(error, "quantize launch failed");
+    qk::MatvecParams p = params_for(xin, nullptr);
+    p.M = static_cast<int32_t>(M);
+    p.K = static_cast<int32_t>(K);
+    p.S = static_cast<int32_t>(K / 256);
+    p.nseg = 2;
+    p.h = h;
+    p.seg[0] = {static_cast<const uint8_t*>(gate), nullptr, static_cast<int32_t>(N), gate_up_type, 0, 0};
+    p.seg[1] = {static_cast<const uint8_t*>(up), nullptr, static_cast<int32_t>(N), gate_up_type, 0, 0};
+    if (static_cast<size_t>(N / 32) * sizeof(uint32_t) <= kFfnArriveBytes) {
+      p.hq = hq;
+      p.arrive = reinterpret_cast<uint32_t*>(base + kFfnQ8Bytes + kFfnNormBytes);
+    }
+    bool fused_q8 = false;
+    hipError_t error = p.hq ? qk::launch_bmv(p, 1, s, fused_q8) : hipSuccess;
+    if (error != hipSuccess) return hip_fail(error, "ffn gate/up launch failed");
+    if (!fused_q8) {
+      status = qk_ffn_gate_up(xin, gate, up, gate_up_type, K, N, h, M, stream);
+      if (status != QK_OK) return status;
+      error = qk::launch_quantize_q8(h, M, N, hq, s);
+      if (error != hipSuccess) return hip_fail(error, "quantize launch failed");
+    }
     return run_single(nullptr, hq, down, down_type, N, K, y, M, s);
   }
   // Otherwise: the fused gate/up (with the norm when given), then down.

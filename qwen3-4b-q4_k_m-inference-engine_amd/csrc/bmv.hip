@@ -10,6 +10,55 @@ namespace qk {
 
 namespace {
 
+// Workgroup owning row r of a segment cut as in bmv_kernel (per rows each,
+// the first rem workgroups one more).
+__device__ __forceinline__ int bmv_owner(int r, int per, int rem) {
+  const int big = rem * (per + 1);
+  return r < big ? r / (per + 1) : rem + (r - big) / per;
+}
+
+// Q8 of h (qk_ffn at M = 2..8) in the gate/up launch. Block b of h (values
+// 32b..32b+31 of every activation row) spans the workgroups that own those
+// rows. Each of them, once its h stores are performed at the memory side
+// (agent-scope stores, then s_waitcnt vmcnt(0) and the workgroup barrier),
+// adds 1 to the block's arrival counter (agent-scope atomic, performed at
+// the memory side); the one whose add completes the owner count resets the
+// counter for the next launch and quantises the block for every activation
+// row, a quad per row, with the quantiser of quantize_q8_kernel (same codes
+// and record bits). Its h loads are agent-scope loads issued after the
+// atomic returned, so they read every owner's stores. No workgroup waits
+// for another, so nothing assumes co-residency.
+__device__ __forceinline__ void bmv_close_blocks(const BmvParams& p, const BmvShare& sh, int N,
+                                                 unsigned char* lds_raw) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's h stores are performed
+  __syncthreads();                                   // ... and every thread's
+  lds_u32* closes = (lds_u32*)(lds_raw);             // the activation codes are no longer read
+  const int tid = static_cast<int>(threadIdx.x);
+  const int b0 = sh.r0 >> 5, nb = ((sh.r0 + sh.nrows - 1) >> 5) - b0 + 1;
+  const int per = sh.per, rem = sh.rem;
+  if (tid < nb) {
+    const int b = b0 + tid;
+    const int owners = bmv_owner(min(32 * b + 31, N - 1), per, rem) - bmv_owner(32 * b, per, rem) + 1;
+    const uint32_t seen =
+        __hip_atomic_fetch_add(p.arrive + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    const bool last = seen == static_cast<uint32_t>(owners);
+    if (last) __hip_atomic_store(p.arrive + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    closes[tid] = last ? 1u : 0u;
+  }
+  __syncthreads();
+  const int M = p.M, q = tid >> 2;  // quad q: block b0 + q / M, activation row q % M
+  if (q >= nb * M) return;           // whole quads
+  const int i = q / M, m = q - i * M;
+  if (closes[i] == 0u) return;
+  const int b = b0 + i;
+  const float* src = p.h + static_cast<int64_t>(m) * N + 32 * b + 8 * (tid & 3);
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = __hip_atomic_load(src + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  store_q8_quarter(p.hq + static_cast<int64_t>(m) * (N / 32) + b, static_cast<uint32_t>(tid & 3),
+                   quantize_quarter(v));
+}
+
 // One type's path of a workgroup: prefetch, quantise, stream, totals.
 template <int TYPE, int MODE, int P>
 __device__ __forceinline__ void bmv_body(const BmvParams& p, const BmvShare& sh, int rows_seg,
@@ -123,8 +172,16 @@ __device__ __forceinline__ void bmv_body(const BmvParams& p, const BmvShare& sh,
       const lds_f32* pb = pa + groups_max * 16 * R * 8;
       float b = 0.0f;
       for (int rr = 0; rr < R; ++rr) b += pb[rr * 8];
-      p.h[static_cast<int64_t>(m) * rows_seg + sh.r0 + row] = (a / (1.0f + expf(-a))) * b;
+      float* dst = p.h + static_cast<int64_t>(m) * rows_seg + sh.r0 + row;
+      const float hv = (a / (1.0f + expf(-a))) * b;
+      if (p.hq != nullptr)  // read back by the workgroup that completes the block
+        __hip_atomic_store(dst, hv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        *dst = hv;
     }
+  }
+  if constexpr (MODE == 1) {
+    if (p.hq != nullptr) bmv_close_blocks(p, sh, rows_seg, lds_raw);
   }
 }
 
@@ -137,7 +194,7 @@ __global__ __launch_bounds__(64 * kBmvWaves) void bmv_kernel(const BmvParams p) 
   for (int j = 0; j < kMaxSegments; ++j)
     asm volatile("" ::"s"(p.seg[j].w), "s"(p.seg[j].y), "s"(p.seg[j].rows), "s"(p.seg[j].type),
                  "s"(p.seg[j].wg_begin), "s"(p.seg[j].per), "s"(p.seg[j].rem), "s"(p.seg[j].pad));
-  asm volatile("" ::"s"(p.x), "s"(p.h), "s"(p.M), "s"(p.K), "s"(p.S), "s"(p.nseg), "s"(p.stride),
+  asm volatile("" ::"s"(p.x), "s"(p.h), "s"(p.hq), "s"(p.arrive), "s"(p.M), "s"(p.K), "s"(p.S), "s"(p.nseg), "s"(p.stride),
                "s"(p.ranges), "s"(p.groups_max), "s"(p.pad));
   __builtin_amdgcn_sched_barrier(0);
   const int wg = static_cast<int>(blockIdx.x), nseg = p.nseg;
@@ -158,6 +215,8 @@ __global__ __launch_bounds__(64 * kBmvWaves) void bmv_kernel(const BmvParams p) 
   sh.w[1] = MODE == 1 ? p.seg[1].w : sh.w[0];
   sh.r0 = g * per + min(g, rem);
   sh.nrows = per + (g < rem ? 1 : 0);
+  sh.per = per;
+  sh.rem = rem;
   sh.groups = (sh.nrows + 15) >> 4;
   sh.S = p.S;
   sh.ranges = p.ranges;
@@ -273,11 +332,20 @@ hipError_t launch_bmv(const MatvecParams& p, int mode, hipStream_t stream, bool&
   if (e != hipSuccess) return e;
   int count[kMaxSegments] = {0}, ranges = 0, groups_max = 0, lds = 0;
   if (!bmv_plan(p, mode, cus, max_lds, count, ranges, groups_max, lds)) return hipSuccess;
+  if (p.hq != nullptr) {  // Q8(h) in the launch: a quad per (block, activation row) of a share
+    const int64_t rows_max = (p.seg[0].rows + count[0] - 1) / count[0];
+    const int64_t blocks = (rows_max + 30) / 32 + 1;  // blocks a run of rows_max rows can touch
+    if (p.seg[0].rows % 32 != 0 || blocks > kBmvMaxCloseBlocks || 4 * blocks * p.M > 64 * kBmvWaves ||
+        p.arrive == nullptr)
+      return hipSuccess;
+  }
 
   const int nseg = mode == 1 ? 1 : p.nseg;
   BmvParams bp{};
   bp.x = p.x;
   bp.h = p.h;
+  bp.hq = p.hq;
+  bp.arrive = p.hq != nullptr ? p.arrive : nullptr;
   bp.M = p.M;
   bp.K = p.K;
   bp.S = p.S;
@@ -299,7 +367,7 @@ hipError_t launch_bmv(const MatvecParams& p, int mode, hipStream_t stream, bool&
   if (!fn) return hipSuccess;
   e = allow_lds(reinterpret_cast<const void*>(fn), lds);
   if (e != hipSuccess) return e;
-  note("bmv_kernel", begin, type, mode, ranges, groups_max);
+  note("bmv_kernel", begin, type, mode, ranges, groups_max, p.hq != nullptr);
   hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(begin)), dim3(64 * kBmvWaves),
                      static_cast<size_t>(lds), stream, bp);
   launched = true;

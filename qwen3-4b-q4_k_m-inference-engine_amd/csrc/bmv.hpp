@@ -53,10 +53,15 @@ constexpr int kBmvXStaged6 = 5;
 constexpr int kBmvP4 = 6;       // Q4_K tiles in flight per wave
 constexpr int kBmvP6 = 4;       // Q6_K tiles in flight per wave
 constexpr int kBmvP6Mixed = 3;  // Q6_K tiles in flight in a launch with both types
+// Q8 blocks of h one workgroup may complete (M activation rows each, a quad
+// per block row): the launcher checks blocks * M * 4 <= threads.
+constexpr int kBmvMaxCloseBlocks = 16;
 
 struct BmvParams {
-  const float* x;  // [M x K]
-  float* h;        // mode 1 output [M x N]
+  const float* x;       // [M x K]
+  float* h;             // mode 1 output [M x N]
+  qk_q8_block* hq;      // mode 1, optional: Q8 of h [M][N/32], formed in the launch
+  uint32_t* arrive;     // with hq: per-block arrival counters [N/32], zero between launches
   int32_t M, K, S, nseg;
   int32_t stride;      // LDS bytes per activation row of codes (K + 16)
   int32_t ranges;      // superblock runs per row group
@@ -70,7 +75,8 @@ struct BmvParams {
 //   zero  16 bytes                 at 8*stride
 //   xs    [K/32][8] fp32 Q8 scale  at Z = 8*stride + 16
 //   xss   [K/32][8] fp32 scale*sum(codes)          at Z + K
-//   xf    [K/16][8] fp32 scale*(-32*sum of 16 codes) at Z + 2K
+//   xf    [K/16][8] int32 -32*(sum of 16 codes)    at Z + 2K (the Q6_K offset,
+//                                                  the MFMA's accumulator input)
 //   sums  [parts][groups_max][16][ranges][8] fp32  at Z + 4K
 // Rows m >= M of every array are left unwritten: they feed only results for
 // activation rows that are never stored.
@@ -79,9 +85,11 @@ __host__ __device__ constexpr int bmv_lds_bytes(int K, int stride, int parts, in
   return bmv_lds_z(stride) + 4 * K + parts * groups * 16 * ranges * 32;
 }
 
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
-typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+typedef __attribute__((address_space(3))) int32_t lds_i32;
 
 // Task t (8 activations of the [M][K] stream): codes to row t / (K/8), the
 // block's scales by lane 0 of its quad.
@@ -95,8 +103,9 @@ __device__ __forceinline__ void bmv_quantize_task(f32x4 a, f32x4 b, int t, int g
     const int blk = k0 >> 5;
     xs[blk * 8 + m] = q.scale;
     xss[blk * 8 + m] = q.scale * static_cast<float>(q.pair + q.other);
-    xf[(2 * blk) * 8 + m] = q.scale * static_cast<float>(-32 * q.pair);
-    xf[(2 * blk + 1) * 8 + m] = q.scale * static_cast<float>(-32 * q.other);
+    lds_i32* xi = reinterpret_cast<lds_i32*>(xf);
+    xi[(2 * blk) * 8 + m] = -32 * q.pair;
+    xi[(2 * blk + 1) * 8 + m] = -32 * q.other;
   }
 }
 
@@ -128,8 +137,8 @@ __device__ __forceinline__ void bmv_load(Q6Tile& t, const uint8_t* sb, int kq) {
   t.d = load_u16(sb + 208);
 }
 
-__device__ __forceinline__ i32x4 mfma_i8(i32x4 a, u32x4 b) {
-  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, __builtin_bit_cast(i32x4, b), i32x4{0, 0, 0, 0}, 0, 0, 0);
+__device__ __forceinline__ i32x4 mfma_i8(i32x4 a, u32x4 b, i32x4 c = i32x4{0, 0, 0, 0}) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
 }
 
 __device__ __forceinline__ i32x4 lds_read_i32x4(const lds_u8* base, uint32_t off) {
@@ -217,7 +226,8 @@ __device__ __forceinline__ void bmv_tile(const Q6Tile& t, int s, const BmvLane& 
 #pragma unroll
     for (int nib = 0; nib < 2; ++nib) {
       // 16 codes (ql nibble | qh pair << 4, 0..63; the -32 offset enters
-      // through xf): src/cuda/matmul.cu:71-79
+      // as the MFMA's accumulator input -32 * sum(activation codes), so the
+      // integer dot is exact): src/cuda/matmul.cu:71-79
       const u32x4 ql = h ? t.lb : t.la;
       const u32x4 qh = h ? t.hb : t.ha;
       const uint32_t sh = nib ? sh1 : sh0;
@@ -234,12 +244,12 @@ __device__ __forceinline__ void bmv_tile(const Q6Tile& t, int s, const BmvLane& 
 #pragma unroll
       for (int mh = 0; mh < MH; ++mh) {
         const uint32_t aoff = L.a6_valid ? L.a6_base + 4 * mh * stride + 256 * s + 128 * h + 64 * nib : L.zero;
-        const i32x4 ci = mfma_i8(lds_read_i32x4(codes, aoff), b);
+        const i32x4 n4 = lds_read_i32x4(reinterpret_cast<const lds_u8*>(xf), 4u * ((16 * s + sb16) * 8 + 4 * mh));
+        const i32x4 ci = mfma_i8(lds_read_i32x4(codes, aoff), b, n4);
         const f32x4 x4 = lds_read_f32x4(xs + (8 * s + blk) * 8 + 4 * mh);
-        const f32x4 f4 = lds_read_f32x4(xf + (16 * s + sb16) * 8 + 4 * mh);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          accsb[mh][i] = __builtin_fmaf(scf, __builtin_fmaf(x4[i], static_cast<float>(ci[i]), f4[i]), accsb[mh][i]);
+          accsb[mh][i] = __builtin_fmaf(scf, x4[i] * static_cast<float>(ci[i]), accsb[mh][i]);
       }
     }
   }
@@ -260,6 +270,7 @@ struct BmvCursor {
 struct BmvShare {
   const uint8_t* w[2];  // per part (mode 1: gate, up)
   int r0, nrows, groups, S, row_bytes, ranges, run_q, run_r;
+  int per, rem;  // the segment's cut: per rows a workgroup, the first rem one more
   __device__ __forceinline__ int run_begin(int rr) const { return rr * run_q + min(rr, run_r); }
 };
 

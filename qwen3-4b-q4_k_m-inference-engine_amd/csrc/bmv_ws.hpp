@@ -109,9 +109,9 @@ __device__ __forceinline__ void ws_tile(Q6Tile& t, const lds_u8* sb, int kq) {
 // Block b of caller-provided Q8 blocks [M][K/32] (its three 16-byte words:
 // codes 0..15, codes 16..31, then scale / scale*sum / -32*sum(0..15) /
 // -32*sum(16..31)) into the LDS image bmv_quantize_task writes: the same
-// codes, the same scale and the same fp32 products of it. The record is bit
-// cast as a whole vector: a bit cast of one subscripted element (rec.y) was
-// compiled as the vector's first element.
+// codes, the same scale, the same fp32 product scale*sum and the same
+// integer offsets. The record is bit cast as a whole vector: a bit cast of
+// one subscripted element (rec.y) was compiled as the vector's first element.
 __device__ __forceinline__ void bmv_store_block(u32x4 c0, u32x4 c1, u32x4 rec, int b, int bpr, int stride,
                                                 lds_u8* codes, lds_f32* xs, lds_f32* xss, lds_f32* xf) {
   const int m = b / bpr, blk = b - m * bpr;
@@ -122,8 +122,9 @@ __device__ __forceinline__ void bmv_store_block(u32x4 c0, u32x4 c1, u32x4 rec, i
   const float scale = rf.x;
   xs[blk * 8 + m] = scale;
   xss[blk * 8 + m] = rf.y;
-  xf[(2 * blk) * 8 + m] = scale * static_cast<float>(static_cast<int32_t>(rec.z));
-  xf[(2 * blk + 1) * 8 + m] = scale * static_cast<float>(static_cast<int32_t>(rec.w));
+  lds_i32* xi = reinterpret_cast<lds_i32*>(xf);
+  xi[(2 * blk) * 8 + m] = static_cast<int32_t>(rec.z);
+  xi[(2 * blk + 1) * 8 + m] = static_cast<int32_t>(rec.w);
 }
 
 // One type's path of a workgroup: rows [r0, r0 + nrows) (nrows <= 16) of a

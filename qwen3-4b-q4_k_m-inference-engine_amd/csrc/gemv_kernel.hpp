@@ -147,6 +147,18 @@ __device__ __forceinline__ Q8Quarter quantize_quarter(const float (&v)[8]) {
   return Q8Quarter{lo, hi, scale, pair, other};
 }
 
+// Quarter `quarter` of a Q8 block record in global memory (qk_q8_block):
+// its 8 codes, and from lane 0 of the quad the 16-byte tail (scale,
+// scale * sum of codes, -32 * sums of codes 0..15 and 16..31).
+__device__ __forceinline__ void store_q8_quarter(qk_q8_block* blk, uint32_t quarter, const Q8Quarter& q) {
+  *reinterpret_cast<u32x2*>(blk->codes + 8 * quarter) = u32x2{q.lo, q.hi};
+  if (quarter == 0) {
+    const f32x4 rec = {q.scale, q.scale * static_cast<float>(q.pair + q.other),
+                       __builtin_bit_cast(float, -32 * q.pair), __builtin_bit_cast(float, -32 * q.other)};
+    *reinterpret_cast<f32x4*>(&blk->scale) = rec;
+  }
+}
+
 __device__ __forceinline__ void quantize_group(const float (&v)[8], lds_q8_block* blk, uint32_t q) {
   const Q8Quarter r = quantize_quarter(v);
   *reinterpret_cast<lds_u32x2*>(blk->codes + 8 * q) = u32x2{r.lo, r.hi};

@@ -52,6 +52,8 @@ struct MatvecParams {
   int32_t pad2;
   void* argmax_ws;              // argmax mode: ArgmaxWorkspace (argmax.hpp)
   uint32_t* argmax_result;      // argmax mode: index of the largest output
+  qk_q8_block* hq;              // FFN mode, batched kernel only: Q8(h) [M][N/32] formed in the launch
+  uint32_t* arrive;             // with hq: per-block arrival counters [N/32], zero between launches
   MatvecSegment seg[kMaxSegments];
 };
 
@@ -77,8 +79,10 @@ hipError_t launch_pass_matvec(const MatvecParams& p, int mode, hipStream_t strea
 hipError_t launch_bmv_ws(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
 
 // The batched mat-vec on the int8 matrix cores (bmv.hip): M = 2..8 rows of
-// fp32 activations, modes 0 and 1; launched (and `launched` set) when the
-// shape fits its LDS plan.
+// fp32 activations, the gate/up mode (1); with p.hq and p.arrive it also
+// writes Q8(h). Launched (and `launched` set) when the shape fits its LDS
+// plan (and, with p.hq, its block-closing step); otherwise nothing is
+// enqueued.
 hipError_t launch_bmv(const MatvecParams& p, int mode, hipStream_t stream, bool& launched);
 
 // The multi-pass batched mat-vec on the int8 matrix cores (bmv_pass.hip): M =

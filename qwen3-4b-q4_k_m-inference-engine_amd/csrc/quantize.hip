@@ -24,15 +24,7 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float* __restric
   const f32x4 a = *reinterpret_cast<const f32x4_a4*>(x + 8 * t);
   const f32x4 b = *reinterpret_cast<const f32x4_a4*>(x + 8 * t + 4);
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  const Q8Quarter q = quantize_quarter(v);
-  qk_q8_block* blk = out + (t >> 2);
-  const uint32_t quarter = static_cast<uint32_t>(t & 3);
-  *reinterpret_cast<u32x2*>(blk->codes + 8 * quarter) = u32x2{q.lo, q.hi};
-  if (quarter == 0) {
-    const f32x4 rec = {q.scale, q.scale * static_cast<float>(q.pair + q.other),
-                       __builtin_bit_cast(float, -32 * q.pair), __builtin_bit_cast(float, -32 * q.other)};
-    *reinterpret_cast<f32x4*>(&blk->scale) = rec;
-  }
+  store_q8_quarter(out + (t >> 2), static_cast<uint32_t>(t & 3), quantize_quarter(v));
 }
 
 }  // namespace

@@ -317,12 +317,12 @@ def emulate(oracle, rows, types, K, mode, M, weights, x, rng):
     zero = np.zeros(16, dtype=np.int64)
     xs = rng.standard_normal((K // 32, 8)) * 1e3
     xss = rng.standard_normal((K // 32, 8)) * 1e3
-    xf = rng.standard_normal((K // 16, 8)) * 1e3
+    xf = rng.integers(-(1 << 20), 1 << 20, size=(K // 16, 8), dtype=np.int64)
     c32 = codes_q.reshape(M, K // 32, 32).astype(np.int64)
     xs[:, :M] = scales_q.T
     xss[:, :M] = (scales_q * c32.sum(axis=2)).T
-    xf[0::2, :M] = (scales_q * (-32 * c32[:, :, :16].sum(axis=2))).T
-    xf[1::2, :M] = (scales_q * (-32 * c32[:, :, 16:].sum(axis=2))).T
+    xf[0::2, :M] = (-32 * c32[:, :, :16].sum(axis=2)).T  # int32: the Q6_K MFMA's accumulator input
+    xf[1::2, :M] = (-32 * c32[:, :, 16:].sum(axis=2)).T
 
     def a_tile(offs):  # A[r][16kq+t] from lane (r, kq) = (l%16, l/16) reading 16 bytes at offs[l]
         A = np.zeros((16, 64), dtype=np.int64)
@@ -415,10 +415,10 @@ def emulate(oracle, rows, types, K, mode, M, weights, x, rng):
                             blk = 4 * h + 2 * nib + khi
                             for mh in range(2 if M > 4 else 1):
                                 A = a_tile(np.where(valid, base + 4 * mh * stride + 256 * s + 128 * h + 64 * nib, 8 * stride))
-                                C = lane_c(A @ Bm)
+                                n4 = np.stack([xf[16 * s + sb16[l], 4 * mh:4 * mh + 4] for l in range(64)])
+                                C = lane_c(A @ Bm) + n4  # D = A B + C, exact in int32
                                 x4 = np.stack([xs[8 * s + blk[l], 4 * mh:4 * mh + 4] for l in range(64)])
-                                f4 = np.stack([xf[16 * s + sb16[l], 4 * mh:4 * mh + 4] for l in range(64)])
-                                accsb[:, 4 * mh:4 * mh + 4] += scf[:, None] * (x4 * C + f4)
+                                accsb[:, 4 * mh:4 * mh + 4] += scf[:, None] * (x4 * C)
                     acc += d[:, None] * accsb
                 if last:
                     if qtype == 12:
@@ -468,3 +468,52 @@ def test_bmv_arithmetic_matches_oracle(oracle, rows, types, K, mode, M):
         u = oracle.reference_product(x, weights[1], types[1], K, rows[1])
         ref = g / (1.0 + np.exp(-g)) * u
         assert oracle.row_norm_error(got[0], ref) <= 1e-6
+
+
+
+def _owner(r, per, rem):
+    big = rem * (per + 1)
+    return r // (per + 1) if r < big else rem + (r - big) // per
+
+
+@pytest.mark.parametrize("N,M,count", [(9728, 8, 256), (9728, 2, 256), (512, 5, 7), (2048, 8, 100),
+                                       (96, 3, 50), (6144, 8, 256), (256, 8, 256)])
+def test_bmv_q8h_blocks_close_once(N, M, count):
+    """Q8(h) in the gate/up launch (bmv_close_blocks): whatever order the
+    workgroups arrive in, each 32-value block of h is completed by exactly one
+    workgroup, after every workgroup owning one of its rows arrived, every
+    counter is back at zero for the next launch, and the closing quads fit the
+    workgroup (the launcher's bound on blocks per share holds)."""
+    count = min(count, N)
+    per, rem = divmod(N, count)
+    rows_max = per + (1 if rem else 0)
+    bound = (rows_max + 30) // 32 + 1
+    if not (N % 32 == 0 and bound <= 16 and 4 * bound * M <= 64 * WAVES):
+        return  # the launcher declines; the separate quantise launch runs
+    rng = np.random.default_rng(N + M + count)
+    for trial in range(3):
+        arrive = np.zeros(N // 32, dtype=np.int64)
+        closed = np.zeros(N // 32, dtype=np.int64)
+        arrived = np.zeros(N // 32, dtype=np.int64)
+        for g in rng.permutation(count):
+            r0, nrows = g * per + min(g, rem), per + (1 if g < rem else 0)
+            b0 = r0 >> 5
+            nb = ((r0 + nrows - 1) >> 5) - b0 + 1
+            assert nb <= bound
+            for i in range(nb):
+                b = b0 + i
+                first, last = _owner(32 * b, per, rem), _owner(min(32 * b + 31, N - 1), per, rem)
+                assert first <= g <= last
+                arrive[b] += 1
+                arrived[b] += 1
+                if arrive[b] == last - first + 1:
+                    arrive[b] = 0
+                    closed[b] += 1
+                    assert arrived[b] == last - first + 1  # every owner's h is stored
+                    quads = [(i * M + m) for m in range(M)]
+                    assert max(quads) * 4 + 3 < 64 * WAVES
+        assert np.all(closed == 1) and np.all(arrive == 0)
+    # the owner function restates the cut
+    for r in range(0, N, max(1, N // 97)):
+        g = _owner(r, per, rem)
+        assert g * per + min(g, rem) <= r < g * per + min(g, rem) + per + (1 if g < rem else 0)

@@ -173,6 +173,31 @@ def test_ffn_block_batched_rows_take_separate_launches(gpu, oracle, M, norm, dow
         assert oracle.row_norm_error(y, y_own) <= 1e-5
 
 
+@pytest.mark.parametrize("M,K,N", [(8, 2560, 9728), (3, 2560, 9728), (8, 1024, 3072)])
+def test_ffn_block_batched_q8h_from_gate_up_launch(gpu, oracle, M, K, N):
+    """M = 2..8: Q8(h) in the workspace (formed in the gate/up launch by the
+    workgroup that completes each 32-value block) equals qk_quantize_q8 of the
+    call's own h bit for bit, and every block arrival counter is zero again
+    after each call (three calls on one workspace). Workspace layout, as
+    qk_ffn_workspace_size documents it: barrier words, Q8(h) 160 KiB, norm rows
+    512 KiB, arrival counters 8 KiB."""
+    blk = Block(gpu, oracle, K, N, Q6, M, True, SEED + 500 + M + N)
+    ws, nbytes = _workspace(gpu)
+    q8_off = nbytes - (160 + 512 + 8) * 1024
+    arrive_off = nbytes - 8 * 1024
+    nq = M * N // 32 * gpu.Q8_BLOCK_BYTES
+    for rep in range(3):
+        h, y, launch = blk.run(ws, nbytes)
+        raw = ws.download(np.uint8)
+        hd = gpu.DeviceBuffer.from_array(h.reshape(-1))
+        q8 = gpu.DeviceBuffer(nq)
+        gpu.quantize_q8(hd, M, N, q8)
+        gpu.synchronize()
+        assert np.array_equal(raw[q8_off:q8_off + nq], q8.download(np.uint8)), f"call {rep}"
+        assert not raw[arrive_off:arrive_off + 4 * (N // 32)].any(), f"call {rep}: counters left set"
+    blk.check(oracle, h, y)
+
+
 @pytest.mark.parametrize("M", [1, 8])
 def test_ffn_block_graph_replays(gpu, oracle, M):
     """The block captured in a graph (M = 1: the one launch; M = 8: norm,

@@ -508,8 +508,8 @@ def test_prologue_quantisation_bitwise(gpu, oracle, M, K):
     assert bad[0].size == 0, f"{bad[0].size} mismatches, first at (m, k) = ({bad[0][0]}, {bad[1][0]})"
 
 
-@pytest.mark.parametrize("name,M", [(name, M) for name in ["attn_q", "attn_v", "attn_output", "ffn_gate"]
-                                    for M in (2, 8)] + [("attn_q", 7), ("attn_v", 7)])
+@pytest.mark.parametrize("name,M", [(name, M) for name in ["attn_q", "attn_v", "attn_output", "ffn_gate", "ffn_down"]
+                                    for M in (2, 8)] + [("attn_q", 7), ("attn_v", 7), ("ffn_down", 5)])
 def test_matmul_q8_batched_qwen3_shapes(gpu, oracle, name, M):
     """qk_quantize_q8 + qk_matmul_q8 (the caller-quantised input of
     src/cuda/matmul.cu's two launches) at M = 2 and 8 on the full Qwen3
