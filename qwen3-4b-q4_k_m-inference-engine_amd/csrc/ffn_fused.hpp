@@ -281,7 +281,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
     out_scale = rsqrtf(total / static_cast<float>(K) + eps);
   }
   // (its last step: wave 15 forms the row totals and stores h)
-  stream_consume<TG, JG, 1, false, NORM, true, kHWave, kFfnHWaves, JG - 1>(
+  stream_consume<TG, JG, 1, true, NORM, true, kHWave, kFfnHWaves, JG - 1>(
       wsg, S, max_sb, r0, r1, nullptr, (global_f32*)(hout), xq, wlds, sums, out_scale, issue_down);
 
   // LDS of phase B: Q8 of h, the down regions of the waves (JD KB each) at

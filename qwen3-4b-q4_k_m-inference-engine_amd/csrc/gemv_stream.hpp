@@ -147,13 +147,14 @@ __device__ __forceinline__ void issue_share(WaveShare<J>& ws, const uint8_t* w, 
 // piece q%4), superblock sums to LDS, a barrier, then the row totals. Only a
 // chunk moved back at the matrix end can sit off a 16-byte boundary.
 // IL: each round right after the chunks it needs (measured faster for the
-// mixed-type q/k/v launch); otherwise every chunk first, then the rounds.
+// mixed-type q/k/v launch and the fused FFN's gate/up phase); otherwise every
+// chunk first, then the rounds.
 // SCALED: row totals are multiplied by out_scale (the RMSNorm fold).
 // AGENT_H: h is stored with agent-scope coherent stores (read back by other
 // workgroups of the same launch, the fused FFN). ROW_WAVE0, ROW_WAVES: the
-// waves that form the row totals. HOOK_AT: when >= 0
-// (non-IL only), hook() runs right after chunk HOOK_AT is in LDS (the fused
-// FFN issues its next loads there, once part of this share has arrived).
+// waves that form the row totals. HOOK_AT: when >= 0, hook() runs right after
+// chunk HOOK_AT is in LDS, before the rounds that chunk completes (the fused
+// FFN issues its next loads there, once its share has arrived).
 // A row's total from its S superblock sums by one lane, in the order of a
 // quad's (lane k adds sums k, k+4, ... in order from 0; then the DPP sums
 // (s0 + s1) + (s2 + s3)), so both give the same bits.
@@ -228,6 +229,11 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       write_chunk(j);
+      if (j == HOOK_AT) {
+        __builtin_amdgcn_sched_barrier(0);  // the hook's loads stay after this chunk's wait
+        hook();
+        __builtin_amdgcn_sched_barrier(0);
+      }
       asm volatile("" ::: "memory");  // the wave's reads below follow its writes
       for (; r < rounds && round_chunks(r) <= 64 * (j + 1); ++r) compute(r);
     }
