@@ -116,7 +116,7 @@ __device__ __forceinline__ void pass_compute(PassRows pr, const PassRun& r, int 
   for (int q0 = 0; q0 < npc; q0 += 64) {
     const int q = q0 + lane;
     const int sbw = min(q, npc - 1) >> 2;  // lanes past the pass redo its last superblock, store nothing
-    const lds_u8* sbp = slot + r.o + sbw * B;
+    const lds_u8* sbp = slot + r.o + __umul24(sbw, B);  // full-rate multiply (sbw < 2^24)
     const lds_q8_block* xr = xq + ((s * 8 + blk_a) & 0xFFFF);
     float v;
     if constexpr (TYPE == QK_TYPE_Q4_K)

@@ -199,7 +199,7 @@ __device__ __forceinline__ void stream_consume(const WaveShare<J>& ws, int S, in
   auto compute = [&](int r) {
     const int q = 64 * r + lane;
     const int sbw = min(q, npc - 1) >> 2;  // lanes past the run redo the last superblock, store nothing
-    const lds_u8* sbp = reg + o + sbw * B;
+    const lds_u8* sbp = reg + o + __umul24(sbw, B);  // full-rate multiply (sbw < 2^24)
     const lds_q8_block* xr = xq + ((s * 8 + blk_a) & 0xFFFF);
     float v;
     if constexpr (TYPE == QK_TYPE_Q4_K)

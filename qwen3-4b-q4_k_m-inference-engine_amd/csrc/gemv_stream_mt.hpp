@@ -92,7 +92,7 @@ __device__ __forceinline__ void stream_mt_consume(const u32x4 (&chunk)[J], const
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
     for (int s = s0; s < s1; ++s) {
-      const lds_u8* sbp = rowp + s * B;
+      const lds_u8* sbp = rowp + __umul24(s, B);  // full-rate multiply (s < 2^24)
       const lds_q8_block* xs = xq + ((s * 8 + blk_a) & 0xFFFF);
       if constexpr (TYPE == QK_TYPE_Q4_K) {
         const Q4KPiece f = lds_q4k_piece(sbp, pc);
