@@ -91,8 +91,8 @@ __device__ __forceinline__ void stream_mt_consume(const u32x4 (&chunk)[J], const
     float acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-    for (int s = s0; s < s1; ++s) {
-      const lds_u8* sbp = rowp + __umul24(s, B);  // full-rate multiply (s < 2^24)
+    const lds_u8* sbp = rowp + s0 * B;
+    for (int s = s0; s < s1; ++s, sbp += B) {
       const lds_q8_block* xs = xq + ((s * 8 + blk_a) & 0xFFFF);
       if constexpr (TYPE == QK_TYPE_Q4_K) {
         const Q4KPiece f = lds_q4k_piece(sbp, pc);
@@ -102,11 +102,19 @@ __device__ __forceinline__ void stream_mt_consume(const u32x4 (&chunk)[J], const
           acc[m] += dot_q4k_piece(f, load_x(xr), load_x(xr + blk_step), pc);
         }
       } else {
-        const Q6KPiece f = lds_q6k_piece(sbp, pc);
+        // the piece unpacked once for all MT rows (the same arithmetic as
+        // dot_q6k_piece per row)
+        const Q6KCodes cd = unpack_q6k_piece(lds_q6k_piece(sbp, pc), pc);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           const lds_q8_block* xr = xs + m * S * 8;
-          acc[m] += dot_q6k_piece(f, load_x(xr), load_x(xr + blk_step), pc);
+          acc[m] += dot_q6k_codes(cd, load_x(xr), load_x(xr + blk_step));
+          // rows in pairs: the pair's sums are formed before the next rows'
+          // LDS reads (IR-level code motion otherwise hoists every row's reads)
+          if (MT > 2 && (m & 1)) {
+            asm volatile("" ::"v"(acc[m - 1]), "v"(acc[m]) : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
     }
