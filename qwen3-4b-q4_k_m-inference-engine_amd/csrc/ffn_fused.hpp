@@ -171,6 +171,16 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
   constexpr int BG = TG == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes;
   constexpr int BD = TD == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes;
   constexpr bool kEarly = PD > 0;  // Q6_K down unpacked ahead of h
+  // Gate/up chunks issued at entry; the rest go out after the activation
+  // barrier. With every chunk issued at entry the activations, requested
+  // first, still arrived ~3.3 us after entry (p50; ~1.1 us with no weight
+  // loads at all): they queue behind the whole chip's weight requests. With 3
+  // of 7 chunks ahead (and 4 after) the activation barrier falls earlier, and
+  // phase A, which is VALU-bound from there, ends earlier: block 14.9-15.0 ->
+  // 14.4-14.5 us, decode step 0.927 -> 0.913-0.916 ms (same process, two
+  // interleaved runs; 1 of 7 measured slower, 2 of 7 between). The same split
+  // made the small whole-share launches slower (attn_qkv 5.1 -> 5.4 us).
+  constexpr int kGuEarly = (3 * JG + 6) / 7;
   static_assert(!kEarly || TD == QK_TYPE_Q6_K, "early unpacking is for Q6_K");
   // Every argument in one scalar-load round (see matvec_kernel).
   asm volatile("" ::"s"(p.x), "s"(p.norm), "s"(p.h), "s"(p.y), "s"(p.gate), "s"(p.up), "s"(p.down),
@@ -225,7 +235,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
     const int nsb = (r1 - r0) * S;
     wsg.sb_a = nsb * wv / kWpp;
     wsg.sb_b = nsb * (wv + 1) / kWpp;
-    issue_share<JG>(wsg, wsg.part ? p.up : p.gate, N, r0, S, BG, lane);
+    issue_share<JG, 0, kGuEarly>(wsg, wsg.part ? p.up : p.gate, N, r0, S, BG, lane);
   }
   // Phase B share: superblocks of down rows [d0, d1) (row-major) for waves
   // 0..14. The loads go out once all of the wave's gate/up chunks are in
@@ -274,6 +284,10 @@ __global__ __launch_bounds__(64 * kStreamWaves) void ffn_fused_kernel(const FfnP
   }
   if (wave < nq) quantize_staged_into_lds<1>(1, K, nq, stage, xq);  // K <= kStreamMaxK: all staged
   __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kGuEarly < JG)  // the rest of the gate/up share
+    issue_share<JG, kGuEarly, JG>(wsg, wsg.part ? p.up : p.gate, N, r0, S, BG, lane);
+  __builtin_amdgcn_sched_barrier(0);
   float out_scale = 1.0f;
   if constexpr (NORM) {
     float total = 0.0f;  // the waves' partials in wave order

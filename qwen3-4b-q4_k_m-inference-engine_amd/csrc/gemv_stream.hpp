@@ -122,9 +122,12 @@ struct WaveShare {
 // matrix end: no byte outside the matrix's dwords is read. (Addresses stay
 // pointer arithmetic on the kernel argument, so the compiler keeps them in
 // the global address space: global loads, whose waits count in order.)
-template <int J>
+// J0, J1: only chunks [J0, J1) are loaded (a share issued in two parts; both
+// calls take the same share arguments).
+template <int J, int J0 = 0, int J1 = J>
 __device__ __forceinline__ void issue_share(WaveShare<J>& ws, const uint8_t* w, int rows, int r0,
                                             int S, int B, int lane) {
+  static_assert(0 <= J0 && J0 < J1 && J1 <= J, "chunk range");
   const int64_t row_bytes = static_cast<int64_t>(S) * B;
   const uint8_t* run = w + r0 * row_bytes + static_cast<int64_t>(ws.sb_b > ws.sb_a ? ws.sb_a : 0) * B;
   ws.o = static_cast<int>(reinterpret_cast<uintptr_t>(run) & 3u);  // 0 or 2 (Q6_K), 0 (Q4_K)
@@ -134,7 +137,7 @@ __device__ __forceinline__ void issue_share(WaveShare<J>& ws, const uint8_t* w, 
   const uint8_t* last = w + ((rows * row_bytes + 3) & ~int64_t{3}) - 16;
   ws.lim = static_cast<int>(last - run4);
 #pragma unroll
-  for (int jj = 0; jj < J; ++jj) {
+  for (int jj = J0; jj < J1; ++jj) {
     const uint8_t* a = run4 + 16 * min(lane + 64 * jj, ws.cmax);
     a = a < last ? a : last;
     ws.chunk[jj] = stream_load16_a4(a);
