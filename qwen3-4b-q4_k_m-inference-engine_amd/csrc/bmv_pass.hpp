@@ -51,7 +51,12 @@ template <int TYPE, int J>
 __device__ __forceinline__ void bp_issue(u32x4 (&buf)[J], const BmvPassParams& p, __amdgpu_buffer_rsrc_t rsrc,
                                          int g, int c0, const int (&run)[J], const int (&q)[J]) {
   constexpr int B = TYPE == QK_TYPE_Q4_K ? kQ4KBytes : kQ6KBytes;
-  constexpr int kNt = 2;  // cache policy: nontemporal (each byte is read once)
+  // Cache policy: default. A run of C superblocks starts and ends inside
+  // 128-byte lines that the row's neighbouring passes (the same wave's next
+  // ones) also read; with the nontemporal hint those lines left the L2 in
+  // between and were fetched again: FETCH_SIZE 1.26x the matrix at M = 8,
+  // 1.03x without the hint (lm_head 97-105 -> 94-98 us).
+  constexpr int kNt = 0;
   const int64_t row_bytes = static_cast<int64_t>(p.S) * B;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
