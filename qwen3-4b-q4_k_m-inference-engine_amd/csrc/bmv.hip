@@ -194,8 +194,8 @@ __global__ __launch_bounds__(64 * kBmvWaves) void bmv_kernel(const BmvParams p) 
   for (int j = 0; j < kMaxSegments; ++j)
     asm volatile("" ::"s"(p.seg[j].w), "s"(p.seg[j].y), "s"(p.seg[j].rows), "s"(p.seg[j].type),
                  "s"(p.seg[j].wg_begin), "s"(p.seg[j].per), "s"(p.seg[j].rem), "s"(p.seg[j].pad));
-  asm volatile("" ::"s"(p.x), "s"(p.h), "s"(p.hq), "s"(p.arrive), "s"(p.M), "s"(p.K), "s"(p.S), "s"(p.nseg), "s"(p.stride),
-               "s"(p.ranges), "s"(p.groups_max), "s"(p.pad));
+  asm volatile("" ::"s"(p.x), "s"(p.h), "s"(p.hq), "s"(p.arrive), "s"(p.M), "s"(p.K), "s"(p.S), "s"(p.nseg),
+               "s"(p.stride), "s"(p.ranges), "s"(p.groups_max), "s"(p.pad));
   __builtin_amdgcn_sched_barrier(0);
   const int wg = static_cast<int>(blockIdx.x), nseg = p.nseg;
   const int j = (nseg > 1 && wg >= p.seg[1].wg_begin) + (nseg > 2 && wg >= p.seg[2].wg_begin) +
