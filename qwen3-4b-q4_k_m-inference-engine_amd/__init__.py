@@ -166,10 +166,27 @@ def declared_symbols() -> list[str]:
     return list(_SIGNATURES)
 
 
+_LAUNCH_LOG: set[str] | None = None
+
+
+def record_launches() -> set[str]:
+    """Start collecting the distinct kernel instantiations launched by the
+    calls of this module (each call's last launch, as last_launch() names it);
+    returns the live set."""
+    global _LAUNCH_LOG
+    if _LAUNCH_LOG is None:
+        _LAUNCH_LOG = set()
+    return _LAUNCH_LOG
+
+
 def check(status: int) -> None:
     if status != QK_OK:
         msg = load().qk_last_error()
         raise QKError(status, msg.decode() if msg else "")
+    if _LAUNCH_LOG is not None:
+        name = last_launch()
+        if name:
+            _LAUNCH_LOG.add(name)
 
 
 def last_launch() -> str:

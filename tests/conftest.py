@@ -41,7 +41,20 @@ def load_oracle():
 def qk():
     mod = load_package()
     mod.load()
+    mod.record_launches()
     return mod
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The distinct kernel instantiations the GPU tests launched through the
+    package (shape-determined; listed so a quiet run still records them)."""
+    mod = sys.modules.get("qk_amd")
+    launches = getattr(mod, "_LAUNCH_LOG", None) or () if mod else ()
+    names = sorted({name.split(" grid=")[0] for name in launches})
+    if names:
+        terminalreporter.write_sep("-", f"{len(names)} kernel instantiations launched")
+        for name in names:
+            terminalreporter.write_line(name)
 
 
 @pytest.fixture(scope="session")
