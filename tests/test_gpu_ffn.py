@@ -137,6 +137,31 @@ def test_ffn_workspace_check_reports_and_clears_a_timeout(gpu, oracle):
     gpu.ffn_workspace_check(ws)
 
 
+def test_ffn_one_workspace_across_shapes_and_row_counts(gpu, oracle):
+    """One workspace shared by interleaved calls the way an engine may share
+    it: the Qwen3 block at M = 1 (the grid barrier's words), another shape at
+    M = 1 (the same words, another grid plan), the batched block at M = 8 (its
+    Q8(h) and block counters) and again M = 1, twice round. Every call equals
+    its separate-launch form bit for bit, the barrier never times out, and
+    the batched block's counters are zero after each call."""
+    ws, nbytes = _workspace(gpu)
+    blocks = [Block(gpu, oracle, 2560, 9728, Q6, 1, False, SEED + 901),
+              Block(gpu, oracle, 1024, 3072, Q6, 1, True, SEED + 902),
+              Block(gpu, oracle, 2560, 9728, Q6, 8, True, SEED + 903),
+              Block(gpu, oracle, 2048, 6144, Q4, 1, False, SEED + 904)]
+    expected = [blk.separate() for blk in blocks]
+    arrive_off = nbytes - 8 * 1024
+    for rnd in range(2):
+        for i, blk in enumerate(blocks):
+            h, y, launch = blk.run(ws, nbytes)
+            print(f"[case] shared workspace round {rnd} block {i} (K={blk.K} N={blk.N} M={blk.M}): {launch}",
+                  flush=True)
+            assert np.array_equal(h, expected[i][0]) and np.array_equal(y, expected[i][1]), (rnd, i)
+            raw = ws.download(np.uint8)
+            assert not raw[arrive_off:arrive_off + 4 * (blk.N // 32)].any(), (rnd, i)
+    gpu.ffn_workspace_check(ws)
+
+
 @pytest.mark.parametrize("K,N,down_type", [(1024, 3072, Q6), (2048, 6144, Q4), (512, 1024, Q6)])
 def test_ffn_block_other_shapes_one_launch(gpu, oracle, K, N, down_type):
     blk = Block(gpu, oracle, K, N, down_type, 1, True, SEED + K + N)
